@@ -1,0 +1,209 @@
+"""Benchmark: segmented attention of the 2B 1024^2 final scale on one MI355X.
+
+One step = one ``fused_real_pruning_flat_segmented_attention`` call of the
+final 64x64 scale (B=2, H=16, D=128, 4096 queries, budget-0.1 slab over the
+6425-token prior; seed 1) with its inputs resident in HBM.  The slab is packed
+once before timing (the final scale appends nothing).  Prints one JSON line.
+
+``value`` is attention TFLOP/s counted as sum_(b,h) 4 L (R_h + L) D with R_h
+the retained prior rows (no padding, no masked lanes).  ``roofline`` prices
+the attention kernel against the bf16 dense MFMA peak, from its average
+launch duration measured with HIP events on the stream it runs on.
+``cpu_baseline`` times the numpy oracle (fp32, the reference CPU path's
+gather + softmax) on the host over the whole step, on rank 0.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
+PEAK_HBM_BPS = 8.0e12     # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--budget", type=float, default=None)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-repeats", type=int, default=3)
+    return ap.parse_args()
+
+
+def time_attention(wl, device, steps, warmup):
+    import torch
+
+    from heatkv_amd import fused_real_pruning_flat_segmented_attention
+    from heatkv_amd import workloads as W
+
+    slab_k, slab_v = W.build_slab(wl, device)
+    st, en, ct = wl.schedule.device_tables(wl.target, device)
+    q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
+    kw = dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
+              segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale)
+    for _ in range(warmup):
+        fused_real_pruning_flat_segmented_attention(**kw)
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.current_stream(device)
+    # (1) K back-to-back steps between two events: time per step
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    t0.record(stream)
+    for _ in range(steps):
+        fused_real_pruning_flat_segmented_attention(**kw)
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    ms_per_step = t0.elapsed_time(t1) / steps
+    # (2) per-launch durations, one event pair around each launch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record(stream)
+        fused_real_pruning_flat_segmented_attention(**kw)
+        b.record(stream)
+    torch.cuda.synchronize(device)
+    kern = [a.elapsed_time(b) for a, b in evs]
+    return ms_per_step, statistics.mean(kern), statistics.median(kern)
+
+
+def time_pack(wl, device, reps=20):
+    """Average duration of the slab fill (all prior appends) and its algorithmic bytes."""
+    import torch
+
+    from heatkv_amd import pack_flat_segments_kv
+
+    sched = wl.schedule
+    B, H, _, D = wl.prior_k.shape
+    slab_k = torch.empty((B, sched.capacity, D), dtype=wl.prior_k.dtype, device=device)
+    slab_v = torch.empty_like(slab_k)
+    calls = []
+    nbytes = 0
+    esz = wl.prior_k.element_size() + wl.prior_v.element_size()
+    for s, plan in wl.prior_append_plans():
+        a, b = sched.scale_ranges[s]
+        sk = wl.prior_k[:, :, a:b].to(device).reshape(B, H * (b - a), D)
+        sv = wl.prior_v[:, :, a:b].to(device).reshape(B, H * (b - a), D)
+        meta = sched.device_plan(plan, device, ("append", s))
+        calls.append(dict(dst_k=slab_k, dst_v=slab_v, src_k=sk, src_v=sv, dst_starts=meta[0],
+                          src_starts=meta[1], lengths=meta[2], max_length=plan.max_length))
+        nbytes += B * plan.slots * D * esz * 2
+    for c in calls:
+        pack_flat_segments_kv(**c)
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.current_stream(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(reps):
+        for c in calls:
+            pack_flat_segments_kv(**c)
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    ms = t0.elapsed_time(t1) / reps
+    return ms, nbytes, len(calls)
+
+
+def cpu_baseline(wl, repeats):
+    """Numpy oracle (fp32) over the whole step on the host cores."""
+    import numpy as np
+
+    from oracle import segmented_attention as oattn
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([int(p.get("num_threads", 1)) for p in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    f = lambda t: t.float().numpy()  # noqa: E731
+    st, en, ct = (t.numpy() for t in wl.tables())
+    # slab as the host sees it: place each live segment's rows at its offset
+    B, H, _, D = wl.prior_k.shape
+    slab_k = np.zeros((B, wl.schedule.capacity, D), np.float32)
+    slab_v = np.zeros_like(slab_k)
+    pk, pv = f(wl.prior_k), f(wl.prior_v)
+    for seg in wl.schedule.live_segments(wl.target):
+        slab_k[:, seg.offset:seg.offset + seg.length] = pk[:, seg.head, seg.scale_start:seg.scale_end]
+        slab_v[:, seg.offset:seg.offset + seg.length] = pv[:, seg.head, seg.scale_start:seg.scale_end]
+    args = (f(wl.q), slab_k, slab_v, st, en, ct, f(wl.cur_k), f(wl.cur_v), wl.softmax_scale)
+    oattn.flat_segmented_attention(*args, heads=[0], batches=[0])  # warm-up
+    times = []
+    for _ in range(repeats):
+        t = time.perf_counter()
+        oattn.flat_segmented_attention(*args)
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    return dict(value=wl.attention_flops() / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"whole step ({wl.name}: B={wl.batch}, H={wl.heads}, L={wl.cur_len}), "
+                       f"numpy fp32 oracle, median of {repeats}", ms_per_step=sec * 1e3)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this path needs no collective); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from heatkv_amd import workloads as W
+
+    device = torch.device("cuda:0")
+    wl = W.config(args.config, budget=args.budget)
+    flops = wl.attention_flops()
+    ms_step, kern_mean, kern_med = time_attention(wl, device, args.steps, args.warmup)
+    achieved = flops / (kern_mean * 1e-3)
+    pack_ms, pack_bytes, pack_calls = time_pack(wl, device)
+    rec = {
+        "metric": "segmented-attn TFLOP/s & % bf16 MFMA peak; ms per scale step (2B, 1024^2)",
+        "value": round(flops / (ms_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": wl.name, "batch": wl.batch, "heads": wl.heads, "head_dim": 128,
+            "cur_len": wl.cur_len, "prior_tokens": wl.prefix, "budget": wl.budget, "seed": wl.seed,
+            "retained_rows_per_head": wl.retained_rows(), "slab_capacity": wl.schedule.capacity,
+            "flops_per_step": flops,
+        },
+        "pct_of_bf16_peak": round(100.0 * achieved / PEAK_BF16_FLOPS, 2),
+        "roofline": {
+            "bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": PEAK_BF16_FLOPS / 1e12,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_FLOPS, 4), "traffic": None,
+            "kernel": "seg_attn_kernel", "kernel_ms_mean": round(kern_mean, 5),
+            "kernel_ms_median": round(kern_med, 5),
+        },
+        "compaction": {
+            "what": f"slab fill: {pack_calls} append launches (every kept prior scale)",
+            "ms": round(pack_ms, 5), "bytes": pack_bytes,
+            "GB/s": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(pack_bytes / (pack_ms * 1e-3) / PEAK_HBM_BPS, 4),
+        },
+    }
+    if not args.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline(wl, args.cpu_repeats)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,21 @@
+"""heatkv_amd -- HeatKV's slab compaction + segmented attention on MI355X (gfx950).
+
+Python operator surface (drop-in names of the reference module
+real_pruning_fused_attention.py) over hand-written HIP kernels in
+libheatkv.so; the static slab layout (offsets, offset tables, copy
+descriptors) is computed on the host like the reference's.
+"""
+
+from .real_pruning_fused_attention import (  # noqa: F401
+    fused_real_pruning_flat_segmented_attention,
+    pack_flat_segments_kv,
+)
+from .slab_schedule import (  # noqa: F401
+    SIDES_1M,
+    SlabSchedule,
+    build_slab_schedule,
+    build_static_slot_schedule,
+    scale_token_ranges,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,110 @@
+"""ctypes binding of libheatkv.so (C ABI in include/heatkv.h).
+
+The library is built in-tree (``heatkv_amd/libheatkv.so``) by
+``heatkv_amd.csrc.build``.  There is no fallback: every entry point raises
+``RuntimeError`` when the library is missing or the device is not a gfx950.
+torch is imported before the library is opened so that the library binds to
+the HIP runtime torch already loaded (both share the soname libamdhip64.so.7).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libheatkv.so")
+
+HKV_OK = 0
+HKV_ERR_INVALID_ARG = -1
+HKV_ERR_UNSUPPORTED = -2
+HKV_ERR_LAUNCH = -3
+HKV_ERR_DEVICE = -4
+
+DTYPE_CODES = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
+
+_lock = threading.Lock()
+_lib = None
+_device_ok: dict[int, bool] = {}
+
+_c_i32 = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_p = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/heatkv.h
+SIGNATURES = {
+    "hkv_version": (_c_i32, []),
+    "hkv_device_ok": (_c_i32, [_c_i32]),
+    "hkv_last_error": (ctypes.c_char_p, []),
+    "hkv_pack_segments": (
+        _c_i32,
+        [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+         _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_p],
+    ),
+    "hkv_segmented_attention": (
+        _c_i32,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
+         _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_p],
+    ),
+}
+
+
+def load():
+    """Open libheatkv.so once and return the ctypes handle (RuntimeError if absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libheatkv.so not found at {LIB_PATH}; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`python heatkv_amd/csrc/build.py`"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    msg = load().hkv_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(code: int) -> None:
+    """Map a negative HKV_ERR_* code to ValueError / RuntimeError."""
+    if code == HKV_OK:
+        return
+    msg = last_error() or f"libheatkv error {code}"
+    if code == HKV_ERR_INVALID_ARG:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def require_device(device: torch.device) -> None:
+    """RuntimeError unless ``device`` is a gfx950 GPU the library can run on."""
+    lib = load()
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ok = _device_ok.get(idx)
+    if ok is None:
+        ok = bool(lib.hkv_device_ok(idx))
+        _device_ok[idx] = ok
+    if not ok:
+        name = torch.cuda.get_device_name(idx) if torch.cuda.is_available() else "none"
+        raise RuntimeError(f"libheatkv.so runs on gfx950 (MI355X) only; device {idx} is {name}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    return DTYPE_CODES.get(dtype, 0)

@@ -1,0 +1,165 @@
+// C ABI of libheatkv.so (declared in include/heatkv.h): argument checks,
+// error codes and messages, then the launches in pack.hip / seg_attn.hip.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/heatkv.h"
+#include "hkv_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int32_t ok() {
+  g_last_error.clear();
+  return HKV_OK;
+}
+
+int32_t elem_bytes(int32_t dt) {
+  switch (dt) {
+    case HKV_DTYPE_F16:
+    case HKV_DTYPE_BF16: return 2;
+    case HKV_DTYPE_F32: return 4;
+    default: return 0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t hkv_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+int32_t hkv_device_ok(int32_t device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+const char* hkv_last_error(void) { return g_last_error.c_str(); }
+
+int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                          int64_t src_batch_stride, int64_t dst_batch_stride, int64_t src_rows,
+                          int64_t dst_rows, int32_t batch, int32_t head_dim,
+                          int32_t k_elem_bytes, int32_t v_elem_bytes,
+                          const int64_t* dst_starts, const int64_t* src_starts,
+                          const int64_t* lengths, int32_t n_items, int32_t max_length,
+                          void* stream) {
+  if (n_items < 0) return fail(HKV_ERR_INVALID_ARG, "n_items must be >= 0 (got %d)", n_items);
+  if (n_items == 0 || max_length <= 0) return ok();
+  if (batch <= 0 || batch > 65535)
+    return fail(HKV_ERR_INVALID_ARG, "batch must be in [1, 65535] (got %d)", batch);
+  if (head_dim <= 0 || head_dim > 128)
+    return fail(HKV_ERR_UNSUPPORTED, "pack_flat_segments_kv currently supports head_dim <= 128");
+  if ((k_elem_bytes != 2 && k_elem_bytes != 4) || (v_elem_bytes != 2 && v_elem_bytes != 4))
+    return fail(HKV_ERR_UNSUPPORTED, "element sizes must be 2 or 4 bytes (got %d, %d)",
+                k_elem_bytes, v_elem_bytes);
+  if (!src_k || !src_v || !dst_k || !dst_v || !dst_starts || !src_starts || !lengths)
+    return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if (src_rows < 0 || dst_rows < 0 || src_batch_stride < 0 || dst_batch_stride < 0)
+    return fail(HKV_ERR_INVALID_ARG, "negative size or stride");
+  if (batch > 1 && (src_batch_stride < src_rows * head_dim || dst_batch_stride < dst_rows * head_dim))
+    return fail(HKV_ERR_INVALID_ARG, "batch stride smaller than rows * head_dim");
+  int64_t limit = max_length;
+  if (limit > dst_rows) limit = dst_rows;
+  if (limit > src_rows) limit = src_rows;
+  if (limit <= 0) return ok();
+  hkv::PackArgs a{};
+  a.src_k = src_k;
+  a.src_v = src_v;
+  a.dst_k = dst_k;
+  a.dst_v = dst_v;
+  a.src_batch_stride = src_batch_stride;
+  a.dst_batch_stride = dst_batch_stride;
+  a.src_rows = src_rows;
+  a.dst_rows = dst_rows;
+  a.dst_starts = dst_starts;
+  a.src_starts = src_starts;
+  a.lengths = lengths;
+  a.batch = batch;
+  a.head_dim = head_dim;
+  a.k_elem_bytes = k_elem_bytes;
+  a.v_elem_bytes = v_elem_bytes;
+  a.n_items = n_items;
+  a.row_limit = static_cast<int32_t>(limit > 0x7fffffffLL ? 0x7fffffffLL : limit);
+  const hipError_t e = hkv::launch_pack(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HKV_ERR_LAUNCH, "pack kernel launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* slab_v,
+                                const int32_t* seg_starts, const int32_t* seg_ends,
+                                const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                void* out, float* lse, int32_t batch, int32_t heads,
+                                int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                int32_t v_dtype, float softmax_scale, int32_t use_exp2,
+                                void* stream) {
+  (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
+  if (head_dim != 128)
+    return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented v1 only supports head_dim=128");
+  if (cur_len <= 0)
+    return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented requires current_len > 0");
+  if (batch <= 0 || heads <= 0)
+    return fail(HKV_ERR_INVALID_ARG, "batch and heads must be positive (got %d, %d)", batch, heads);
+  if (elem_bytes(q_dtype) == 0 || elem_bytes(k_dtype) == 0 || elem_bytes(v_dtype) == 0)
+    return fail(HKV_ERR_UNSUPPORTED,
+                "real_scale_fused_segmented supports only float16, bfloat16, or float32 tensors");
+  if (q_dtype != k_dtype)
+    return fail(HKV_ERR_UNSUPPORTED, "q and k must share one dtype (got %d and %d)", q_dtype, k_dtype);
+  if (max_segments < 0 || max_segments > hkv::kMaxSegments)
+    return fail(HKV_ERR_UNSUPPORTED, "max_segments must be in [0, %d] (got %d)", hkv::kMaxSegments,
+                max_segments);
+  if (slab_capacity < 0) return fail(HKV_ERR_INVALID_ARG, "slab_capacity must be >= 0");
+  // Retained prior rows plus current rows index an int32 key stream.
+  if (slab_capacity * static_cast<int64_t>(max_segments > 0 ? max_segments : 1) + cur_len >
+      0x7fffffffLL)
+    return fail(HKV_ERR_UNSUPPORTED, "slab_capacity * max_segments + current_len exceeds 2^31");
+  if (!q || !cur_k || !cur_v || !out || !seg_counts || (max_segments > 0 && (!seg_starts || !seg_ends)))
+    return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if (slab_capacity > 0 && (!slab_k || !slab_v))
+    return fail(HKV_ERR_INVALID_ARG, "null slab pointer with nonzero capacity");
+  hkv::AttnArgs a{};
+  a.q = q;
+  a.slab_k = slab_k;
+  a.slab_v = slab_v;
+  a.seg_starts = seg_starts;
+  a.seg_ends = seg_ends;
+  a.seg_counts = seg_counts;
+  a.cur_k = cur_k;
+  a.cur_v = cur_v;
+  a.out = out;
+  a.lse = lse;
+  a.slab_capacity = slab_capacity;
+  a.batch = batch;
+  a.heads = heads;
+  a.cur_len = cur_len;
+  a.max_segments = max_segments;
+  a.softmax_scale = softmax_scale;
+  a.q_dtype = q_dtype;
+  a.k_dtype = k_dtype;
+  a.v_dtype = v_dtype;
+  const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

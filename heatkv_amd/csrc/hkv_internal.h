@@ -1,0 +1,60 @@
+// Internal launch interface shared by the kernel translation units and the
+// C ABI in abi.hip.  Not installed; the public surface is include/heatkv.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hkv {
+
+struct PackArgs {
+  const void* src_k;
+  const void* src_v;
+  void* dst_k;
+  void* dst_v;
+  int64_t src_batch_stride;  // elements
+  int64_t dst_batch_stride;  // elements
+  int64_t src_rows;
+  int64_t dst_rows;
+  const int64_t* dst_starts;
+  const int64_t* src_starts;
+  const int64_t* lengths;
+  int32_t batch;
+  int32_t head_dim;
+  int32_t k_elem_bytes;
+  int32_t v_elem_bytes;
+  int32_t n_items;
+  int32_t row_limit;  // rows copied per item at most
+};
+
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
+
+enum Dtype : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3 };
+
+struct AttnArgs {
+  const void* q;
+  const void* slab_k;
+  const void* slab_v;
+  const int32_t* seg_starts;
+  const int32_t* seg_ends;
+  const int32_t* seg_counts;
+  const void* cur_k;
+  const void* cur_v;
+  void* out;
+  float* lse;
+  int64_t slab_capacity;
+  int32_t batch;
+  int32_t heads;
+  int32_t cur_len;
+  int32_t max_segments;
+  float softmax_scale;
+  int32_t q_dtype;
+  int32_t k_dtype;
+  int32_t v_dtype;
+};
+
+constexpr int kMaxSegments = 256;
+
+hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream);
+
+}  // namespace hkv

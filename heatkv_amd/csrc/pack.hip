@@ -1,0 +1,124 @@
+// Slab pack / append kernel for gfx950.
+//
+// Semantics follow _pack_flat_segments_kv_kernel
+// (real_pruning_fused_attention.py:33-73): item i copies lengths[i] rows of
+// head_dim elements from src[b, src_starts[i]...] to dst[b, dst_starts[i]...]
+// for K and V.  Rows of one item are consecutive in both tensors, so one
+// (item, batch row) is a single contiguous byte range per tensor; the kernel
+// is a batched memcpy that moves each range in 16-byte vectors when the
+// pointers and row pitch allow it (128-bit loads and stores), else in 4- or
+// 2-byte words.  The copy is bit-exact by construction.
+//
+// Work split: one workgroup of 256 threads per (item, 64-row chunk, batch
+// row).  For bf16 D=128 a chunk is 16 KiB of K plus 16 KiB of V, four
+// independent 16-byte loads in flight per thread per tensor.  Workgroups whose
+// chunk lies beyond their item's length exit at once (append items all share
+// one length, so none are idle there).
+#include "hkv_internal.h"
+
+namespace hkv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunkRows = 64;
+constexpr int kUnroll = 4;
+
+struct alignas(16) U16B { uint32_t w[4]; };
+
+template <typename U>
+__device__ __forceinline__ void copy_range(char* __restrict__ dst, const char* __restrict__ src,
+                                           int64_t bytes) {
+  const int64_t n = bytes / static_cast<int64_t>(sizeof(U));
+  U* d = reinterpret_cast<U*>(dst);
+  const U* s = reinterpret_cast<const U*>(src);
+  int64_t i = threadIdx.x;
+  // Unrolled body: kUnroll loads issued before the stores.
+  for (; i + (kUnroll - 1) * kThreads < n; i += kUnroll * kThreads) {
+    U v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = s[i + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) d[i + u * kThreads] = v[u];
+  }
+  for (; i < n; i += kThreads) d[i] = s[i];
+}
+
+template <typename UK, typename UV>
+__global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs a, int32_t chunks) {
+  const int32_t item = blockIdx.x / chunks;
+  const int32_t chunk = blockIdx.x - item * chunks;
+  const int64_t b = blockIdx.y;
+  int64_t len = a.lengths[item];
+  if (len > a.row_limit) len = a.row_limit;
+  const int64_t r0 = static_cast<int64_t>(chunk) * kChunkRows;
+  if (r0 >= len) return;
+  const int64_t r1 = (r0 + kChunkRows < len) ? r0 + kChunkRows : len;
+  const int64_t s0 = a.src_starts[item] + r0;
+  const int64_t d0 = a.dst_starts[item] + r0;
+  // Clip the row range so that both the source and the destination row stay
+  // inside their tensors.
+  int64_t lo = 0;
+  if (-s0 > lo) lo = -s0;
+  if (-d0 > lo) lo = -d0;
+  int64_t hi = r1 - r0;
+  if (a.src_rows - s0 < hi) hi = a.src_rows - s0;
+  if (a.dst_rows - d0 < hi) hi = a.dst_rows - d0;
+  if (hi <= lo) return;
+  const int64_t rows = hi - lo;
+  const int64_t D = a.head_dim;
+  const int64_t src_elem = b * a.src_batch_stride + (s0 + lo) * D;
+  const int64_t dst_elem = b * a.dst_batch_stride + (d0 + lo) * D;
+  copy_range<UK>(static_cast<char*>(a.dst_k) + dst_elem * a.k_elem_bytes,
+                 static_cast<const char*>(a.src_k) + src_elem * a.k_elem_bytes,
+                 rows * D * a.k_elem_bytes);
+  copy_range<UV>(static_cast<char*>(a.dst_v) + dst_elem * a.v_elem_bytes,
+                 static_cast<const char*>(a.src_v) + src_elem * a.v_elem_bytes,
+                 rows * D * a.v_elem_bytes);
+}
+
+// Widest copy unit (16, 4 or 2 bytes) that keeps every access aligned.
+int unit_bytes(const void* src, const void* dst, int64_t src_bs, int64_t dst_bs, int32_t D,
+               int32_t esize) {
+  const int cands[3] = {16, 4, 2};
+  for (int u : cands) {
+    if (u < esize && u != 16) continue;
+    const bool ok = (reinterpret_cast<uintptr_t>(src) % u == 0) &&
+                    (reinterpret_cast<uintptr_t>(dst) % u == 0) &&
+                    ((static_cast<int64_t>(D) * esize) % u == 0) &&
+                    ((src_bs * esize) % u == 0) && ((dst_bs * esize) % u == 0);
+    if (ok) return u;
+  }
+  return esize;
+}
+
+template <typename UK>
+hipError_t launch_v(const PackArgs& a, int uv, dim3 grid, int32_t chunks, hipStream_t st) {
+  switch (uv) {
+    case 16: pack_kernel<UK, U16B><<<grid, kThreads, 0, st>>>(a, chunks); break;
+    case 4: pack_kernel<UK, uint32_t><<<grid, kThreads, 0, st>>>(a, chunks); break;
+    default: pack_kernel<UK, uint16_t><<<grid, kThreads, 0, st>>>(a, chunks); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream) {
+  if (a.n_items <= 0 || a.row_limit <= 0 || a.batch <= 0) return hipSuccess;
+  const int64_t chunks64 = (static_cast<int64_t>(a.row_limit) + kChunkRows - 1) / kChunkRows;
+  const int64_t blocks = chunks64 * a.n_items;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const int32_t chunks = static_cast<int32_t>(chunks64);
+  dim3 grid(static_cast<uint32_t>(blocks), static_cast<uint32_t>(a.batch), 1);
+  const int uk = unit_bytes(a.src_k, a.dst_k, a.src_batch_stride, a.dst_batch_stride,
+                            a.head_dim, a.k_elem_bytes);
+  const int uv = unit_bytes(a.src_v, a.dst_v, a.src_batch_stride, a.dst_batch_stride,
+                            a.head_dim, a.v_elem_bytes);
+  switch (uk) {
+    case 16: return launch_v<U16B>(a, uv, grid, chunks, stream);
+    case 4: return launch_v<uint32_t>(a, uv, grid, chunks, stream);
+    default: return launch_v<uint16_t>(a, uv, grid, chunks, stream);
+  }
+}
+
+}  // namespace hkv

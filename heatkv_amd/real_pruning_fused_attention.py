@@ -1,0 +1,267 @@
+"""Operator surface of the fused segmented path, on gfx950 HIP kernels.
+
+Drop-in for the reference module real_pruning_fused_attention.py: same
+function names, keyword-only signatures, argument meaning, validation order
+and error types/messages.  The work runs in libheatkv.so (C ABI in
+include/heatkv.h) on the current HIP stream; nothing here synchronises.
+
+Differences from the reference, all deliberate:
+
+* ``fused_real_pruning_flat_segmented_attention(..., return_lse=True)``
+  additionally returns the fp32 softmax log-sum-exp ``[B, H, L]``; the
+  default return value is unchanged.
+* There is no CPU path.  The reference answers ``allow_cpu_fallback=True``
+  with a pure-torch loop (real_pruning_fused_attention.py:509-521); this
+  module raises ``RuntimeError`` for non-GPU tensors either way, so a result
+  is always the HIP kernel's.
+* Tile-shape knobs (``REAL_PRUNING_FUSED_BLOCK_M``/``_BLOCK_N``/
+  ``_NUM_WARPS``/``_NUM_STAGES``) are read and validated like the
+  reference's but the kernel's tile shape is fixed by its MFMA layout.  The
+  dot-mode knobs are validated the same way (``ValueError`` on unknown
+  values); products always take 16-bit MFMA operands (bf16, or fp16 when the
+  inputs are fp16) with fp32 accumulation, which is the reference's default
+  ``bf16`` mode.  fp32 inputs are rounded to bf16 operands.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def _positive_int_env(name: str, default: int) -> int:
+    """Integer env knob, falling back to ``default`` (real_pruning_fused_attention.py:274-283)."""
+    raw = os.environ.get(name)
+    if raw is None:
+        return int(default)
+    try:
+        value = int(raw)
+    except ValueError:
+        return int(default)
+    return value if value > 0 else int(default)
+
+
+def _fused_value_dot_mode_id() -> int:
+    """PV dot mode knob (real_pruning_fused_attention.py:286-295)."""
+    mode = os.environ.get("REAL_PRUNING_FUSED_VALUE_DOT_MODE", "bf16").strip().lower()
+    if mode in {"bf16", "flash"}:
+        return 0
+    if mode in {"fp32", "ieee", "mixed", "fp32_probs"}:
+        return 2
+    raise ValueError("REAL_PRUNING_FUSED_VALUE_DOT_MODE must be one of: bf16, fp32")
+
+
+def _fused_qk_dot_mode_id() -> int:
+    """QK dot mode knob (real_pruning_fused_attention.py:298-308)."""
+    mode = os.environ.get("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16").strip().lower()
+    if mode in {"bf16", "tensorcore"}:
+        return 0
+    if mode in {"tf32", "fp32_tf32"}:
+        return 1
+    if mode in {"fp32", "ieee"}:
+        return 2
+    raise ValueError("REAL_PRUNING_FUSED_QK_DOT_MODE must be one of: bf16, tf32, fp32")
+
+
+def pack_flat_segments_kv(
+    *,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    dst_starts: torch.Tensor,
+    src_starts: torch.Tensor,
+    lengths: torch.Tensor,
+    max_length: Optional[int] = None,
+    block_t: int = 32,
+):
+    """Copy K/V row segments into the slab in place; returns ``(dst_k, dst_v)``.
+
+    Item ``i`` copies ``lengths[i]`` rows from ``src[:, src_starts[i]:]`` to
+    ``dst[:, dst_starts[i]:]`` for K and V.  Mirrors pack_flat_segments_kv
+    (real_pruning_fused_attention.py:365-441); the copy is the HIP kernel
+    ``hkv_pack_segments``.
+    """
+    for name, tensor in (("dst_k", dst_k), ("dst_v", dst_v), ("src_k", src_k), ("src_v", src_v)):
+        if tensor.ndim != 3:
+            raise ValueError(f"pack_flat_segments_kv expects {name} shaped [B, S, D]")
+    if dst_k.shape != dst_v.shape:
+        raise ValueError("pack_flat_segments_kv requires matching K/V destination shapes")
+    if src_k.shape != src_v.shape:
+        raise ValueError("pack_flat_segments_kv requires matching K/V source shapes")
+    if dst_k.shape[0] != src_k.shape[0] or dst_k.shape[2] != src_k.shape[2]:
+        raise ValueError("pack_flat_segments_kv requires matching batch and head_dim")
+    if not all(t.is_cuda for t in (dst_k, dst_v, src_k, src_v)):
+        raise RuntimeError("pack_flat_segments_kv requires CUDA tensors")
+    _lib.load()
+    if dst_starts.numel() == 0:
+        return dst_k, dst_v
+    if (
+        dst_starts.device != dst_k.device
+        or src_starts.device != dst_k.device
+        or lengths.device != dst_k.device
+    ):
+        raise ValueError("pack segment metadata tensors must be on the destination device")
+    if dst_starts.numel() != src_starts.numel() or dst_starts.numel() != lengths.numel():
+        raise ValueError("pack segment metadata tensors must have matching lengths")
+    if not dst_k.is_contiguous() or not dst_v.is_contiguous():
+        raise ValueError("pack_flat_segments_kv requires contiguous destination tensors")
+    if not src_k.is_contiguous():
+        src_k = src_k.contiguous()
+    if not src_v.is_contiguous():
+        src_v = src_v.contiguous()
+    head_dim = int(dst_k.shape[2])
+    if head_dim > 128:
+        raise RuntimeError("pack_flat_segments_kv currently supports head_dim <= 128")
+    if src_k.dtype != dst_k.dtype or src_v.dtype != dst_v.dtype:
+        raise ValueError("pack_flat_segments_kv requires matching source/destination dtypes")
+    max_len = int(max_length) if max_length is not None else int(lengths.max().item())
+    if max_len <= 0:
+        return dst_k, dst_v
+    block_t = int(block_t)
+    if block_t <= 0:
+        raise ValueError("block_t must be positive")
+    row_limit = -(-max_len // block_t) * block_t
+    _lib.require_device(dst_k.device)
+    meta = [t if t.dtype == torch.int64 else t.to(torch.int64) for t in (dst_starts, src_starts, lengths)]
+    meta = [t.contiguous() for t in meta]
+    n_items = int(meta[0].numel())
+    code = _lib.load().hkv_pack_segments(
+        src_k.data_ptr(), src_v.data_ptr(), dst_k.data_ptr(), dst_v.data_ptr(),
+        int(src_k.stride(0)), int(dst_k.stride(0)),
+        int(src_k.shape[1]), int(dst_k.shape[1]),
+        int(dst_k.shape[0]), head_dim,
+        int(dst_k.element_size()), int(dst_v.element_size()),
+        meta[0].data_ptr(), meta[1].data_ptr(), meta[2].data_ptr(),
+        n_items, min(row_limit, 2**31 - 1),
+        _lib.stream_handle(dst_k.device),
+    )
+    _lib.check(code)
+    return dst_k, dst_v
+
+
+def fused_real_pruning_flat_segmented_attention(
+    *,
+    q: torch.Tensor,
+    persisted_k: Optional[torch.Tensor],
+    persisted_v: Optional[torch.Tensor],
+    segment_starts: torch.Tensor,
+    segment_ends: torch.Tensor,
+    segment_counts: torch.Tensor,
+    current_k: torch.Tensor,
+    current_v: torch.Tensor,
+    softmax_scale: float,
+    allow_cpu_fallback: bool = False,
+    softmax_mode: str = "exp",
+    return_lse: bool = False,
+):
+    """Attention of the current scale over the flat slab segments plus itself.
+
+    ``persisted_k/v`` are ``[B, capacity, D]``; ``segment_starts/ends [H, S]``
+    are row offsets into that slab grouped per head, ``segment_counts [H]``.
+    Returns ``[B, L, H*D]`` in q's dtype (and ``lse [B, H, L]`` fp32 when
+    ``return_lse``).  Mirrors fused_real_pruning_flat_segmented_attention
+    (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
+    ``hkv_segmented_attention``.
+    """
+    if q.ndim != 4 or current_k.ndim != 4 or current_v.ndim != 4:
+        raise ValueError("q, current_k, and current_v must have shape [B, H, L, D]")
+    if q.shape != current_k.shape or q.shape != current_v.shape:
+        raise ValueError("q, current_k, and current_v must have identical [B, H, L, D] shapes")
+    if q.device != current_k.device or q.device != current_v.device:
+        raise ValueError("q, current_k, and current_v must be on the same device")
+    if persisted_k is None or persisted_v is None:
+        batch_size = current_k.shape[0]
+        head_dim = current_k.shape[3]
+        persisted_k = current_k.new_empty((batch_size, 0, head_dim))
+        persisted_v = current_v.new_empty((batch_size, 0, head_dim))
+    if persisted_k.ndim != 3 or persisted_v.ndim != 3:
+        raise ValueError("persisted_k and persisted_v must have shape [B, S, D]")
+    if persisted_k.shape != persisted_v.shape:
+        raise ValueError("persisted_k and persisted_v must have identical shapes")
+    if persisted_k.shape[0] != q.shape[0]:
+        raise ValueError("persisted K/V batch dimension must match q")
+    if persisted_k.shape[2] != q.shape[3]:
+        raise ValueError("persisted K/V head_dim must match q")
+    if persisted_k.device != q.device or persisted_v.device != q.device:
+        raise ValueError("persisted K/V must be on the same device as q")
+    if persisted_k.dtype != current_k.dtype:
+        raise ValueError("persisted_k dtype must match current_k")
+    if persisted_v.dtype != current_v.dtype:
+        raise ValueError("persisted_v dtype must match current_v")
+
+    batch_size, num_heads, current_len, head_dim = q.shape
+    if segment_starts.shape != segment_ends.shape:
+        raise ValueError("segment_starts and segment_ends must have identical shapes")
+    if segment_starts.ndim != 2 or segment_starts.shape[0] != num_heads:
+        raise ValueError("segment_starts must have shape [H, S]")
+    if tuple(segment_counts.shape) != (num_heads,):
+        raise ValueError("segment_counts must have shape [H]")
+    if (
+        segment_starts.device != q.device
+        or segment_ends.device != q.device
+        or segment_counts.device != q.device
+    ):
+        raise ValueError("segment metadata must be on the same device as q")
+    if softmax_mode not in {"exp", "exp2"}:
+        raise ValueError(f"unsupported softmax_mode {softmax_mode!r}")
+
+    if q.device.type != "cuda":
+        # No host implementation ships with this library (see module docstring).
+        raise RuntimeError("real_scale_fused_segmented requires CUDA tensors")
+
+    _lib.load()
+    if head_dim != 128:
+        raise RuntimeError("real_scale_fused_segmented v1 only supports head_dim=128")
+    if current_len <= 0:
+        raise RuntimeError("real_scale_fused_segmented requires current_len > 0")
+    for what, t in (("q", q), ("k", current_k), ("v", current_v)):
+        if t.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise RuntimeError(
+                f"real_scale_fused_segmented supports only float16, bfloat16, or float32 {what} tensors"
+            )
+    if q.dtype != current_k.dtype:
+        raise RuntimeError("real_scale_fused_segmented requires q and k of one dtype")
+
+    # Knobs are validated like the reference's (bad values raise ValueError).
+    for knob, default in (("REAL_PRUNING_FUSED_BLOCK_M", 64), ("REAL_PRUNING_FUSED_BLOCK_N", 64),
+                          ("REAL_PRUNING_FUSED_NUM_WARPS", 4), ("REAL_PRUNING_FUSED_NUM_STAGES", 3)):
+        _positive_int_env(knob, default)
+    _fused_qk_dot_mode_id()
+    _fused_value_dot_mode_id()
+
+    _lib.require_device(q.device)
+    q = q.contiguous()
+    persisted_k = persisted_k.contiguous()
+    persisted_v = persisted_v.contiguous()
+    segment_starts = segment_starts.to(dtype=torch.int32).contiguous()
+    segment_ends = segment_ends.to(dtype=torch.int32).contiguous()
+    segment_counts = segment_counts.to(dtype=torch.int32).contiguous()
+    current_k = current_k.contiguous()
+    current_v = current_v.contiguous()
+
+    output = q.new_empty((batch_size, current_len, num_heads * head_dim))
+    lse = (
+        torch.empty((batch_size, num_heads, current_len), device=q.device, dtype=torch.float32)
+        if return_lse
+        else None
+    )
+    code = _lib.load().hkv_segmented_attention(
+        q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
+        segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
+        current_k.data_ptr(), current_v.data_ptr(), output.data_ptr(),
+        lse.data_ptr() if lse is not None else None,
+        batch_size, num_heads, current_len,
+        int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
+        _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
+        float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
+        _lib.stream_handle(q.device),
+    )
+    _lib.check(code)
+    if return_lse:
+        return output, lse
+    return output

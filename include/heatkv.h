@@ -1,0 +1,107 @@
+/*
+ * heatkv.h -- C ABI of libheatkv.so, the MI355X (gfx950) kernels behind the
+ * HeatKV slab-compaction + segmented-attention path.
+ *
+ * Plain pointers and sizes only.  Every device pointer is a HIP device
+ * address; `stream` is a hipStream_t passed as void* (NULL = null stream).
+ * All calls are asynchronous on `stream`, allocate nothing, and return
+ * HKV_OK (0) or a negative HKV_ERR_* code; hkv_last_error() then holds a
+ * message for the calling thread.
+ */
+#ifndef HEATKV_H
+#define HEATKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HKV_OK 0
+#define HKV_ERR_INVALID_ARG (-1)  /* maps to ValueError in the Python layer */
+#define HKV_ERR_UNSUPPORTED (-2)  /* maps to RuntimeError (dtype / head_dim / sizes) */
+#define HKV_ERR_LAUNCH (-3)       /* kernel launch failed (RuntimeError) */
+#define HKV_ERR_DEVICE (-4)       /* no gfx950 device / runtime failure (RuntimeError) */
+
+/* Element types (match torch.float16 / torch.bfloat16 / torch.float32). */
+#define HKV_DTYPE_F16 1
+#define HKV_DTYPE_BF16 2
+#define HKV_DTYPE_F32 3
+
+/* Library version, (major << 16) | (minor << 8) | patch. Loader check. */
+int32_t hkv_version(void);
+
+/* 1 when `device` is a gfx950 GPU this build can run on, else 0.
+ * Loader check; the reference probes Triton/CUDA availability instead
+ * (real_pruning_fused_attention.py:393-396, 522-525). */
+int32_t hkv_device_ok(int32_t device);
+
+/* Message for the last failing call on this thread ("" when none). */
+const char* hkv_last_error(void);
+
+/*
+ * Slab pack / append: for every item i < n_items and batch row b < batch
+ *   dst_k[b, dst_starts[i] + t, :] = src_k[b, src_starts[i] + t, :]
+ *   dst_v[b, dst_starts[i] + t, :] = src_v[b, src_starts[i] + t, :]
+ * for t < lengths[i]; rows outside the items are not written.
+ *
+ * Replaces pack_flat_segments_kv / _pack_flat_segments_kv_kernel
+ * (real_pruning_fused_attention.py:365-441, 33-73).
+ *   src_*  : [batch, *, head_dim] rows, batch stride src_batch_stride elements
+ *   dst_*  : [batch, *, head_dim] rows, batch stride dst_batch_stride elements
+ *   k_elem_bytes / v_elem_bytes : 2 or 4 (K and V may differ, e.g. fp32 K)
+ *   dst_starts, src_starts, lengths : int64 device arrays of n_items
+ *   src_rows / dst_rows : rows per batch of src / dst; a row outside
+ *                [0, rows) is skipped (the reference's kernel does not check;
+ *                this keeps bad descriptors from writing outside the slab)
+ *   max_length : rows copied per item at most.  The reference's grid covers
+ *                ceil(max_length / block_t) tiles of block_t rows, so its
+ *                Python wrapper passes block_t * ceil(max_length / block_t).
+ * head_dim <= 128 as in the reference (:415-416).
+ */
+int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                          int64_t src_batch_stride, int64_t dst_batch_stride,
+                          int64_t src_rows, int64_t dst_rows,
+                          int32_t batch, int32_t head_dim,
+                          int32_t k_elem_bytes, int32_t v_elem_bytes,
+                          const int64_t* dst_starts, const int64_t* src_starts,
+                          const int64_t* lengths, int32_t n_items, int32_t max_length,
+                          void* stream);
+
+/*
+ * Segmented attention over a flat slab plus the current scale:
+ *   out[b, l, h*D:(h+1)*D] = softmax(scale * q[b,h,l] . K_bh^T) V_bh
+ * where K_bh = slab_k[b, starts[h,i]:ends[h,i]] for i < counts[h] (entries
+ * with start >= end skipped), then cur_k[b, h]; V_bh likewise.
+ *
+ * Replaces fused_real_pruning_flat_segmented_attention /
+ * _fused_real_pruning_segmented_attention_kernel
+ * (real_pruning_fused_attention.py:445-591, 76-267).
+ *   q, cur_k, cur_v : [batch, heads, cur_len, head_dim] contiguous
+ *   slab_k, slab_v  : [batch, slab_capacity, head_dim] contiguous
+ *   seg_starts, seg_ends : int32 [heads, max_segments]; seg_counts : int32 [heads]
+ *   out  : [batch, cur_len, heads*head_dim], element type q_dtype
+ *   lse  : NULL, or float32 [batch, heads, cur_len] natural-log log-sum-exp
+ *          of the scaled scores (not produced by the reference kernel)
+ *   *_dtype : HKV_DTYPE_*; slab and current K share k_dtype, V share v_dtype
+ *   use_exp2 : the reference's softmax_mode ("exp" = 0, "exp2" = 1); both give
+ *              the same mathematical result and this kernel always evaluates
+ *              exp2 with scale*log2(e) folded in.
+ * head_dim must be 128 and cur_len > 0 (:526-529).  Segment bounds are
+ * clamped to [0, slab_capacity) and counts to [0, max_segments], so bad
+ * tables cannot address outside the slab.  max_segments <= 256.
+ */
+int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* slab_v,
+                                const int32_t* seg_starts, const int32_t* seg_ends,
+                                const int32_t* seg_counts, const void* cur_k,
+                                const void* cur_v, void* out, float* lse,
+                                int32_t batch, int32_t heads, int32_t cur_len,
+                                int64_t slab_capacity, int32_t max_segments, int32_t head_dim,
+                                int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                float softmax_scale, int32_t use_exp2, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HEATKV_H */

@@ -1,0 +1,241 @@
+"""GPU parity: HIP pack + segmented attention (through the C ABI) against the oracle.
+
+Every call goes through heatkv_amd's Python surface into libheatkv.so.
+Attention is checked against oracle/segmented_attention.py (fp32 numpy) with
+the contract tolerances (out max-abs 2e-2, mean-abs 2e-3, LSE max-abs 1e-3);
+slab packing and offset tables bit-exact against oracle/slot_schedule.py and
+oracle/pack.py.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from heatkv_amd import fused_real_pruning_flat_segmented_attention, pack_flat_segments_kv
+from heatkv_amd import workloads as W
+from oracle import pack as opack
+from oracle import segmented_attention as oattn
+from oracle import slot_schedule as osched
+from support import assert_attention_close, bits, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, slab_k, slab_v, tables, ck, cv, scale, device, **kw):
+    st, en, ct = (t.to(device) for t in tables)
+    out, lse = fused_real_pruning_flat_segmented_attention(
+        q=q.to(device), persisted_k=None if slab_k is None else slab_k.to(device),
+        persisted_v=None if slab_v is None else slab_v.to(device),
+        segment_starts=st, segment_ends=en, segment_counts=ct,
+        current_k=ck.to(device), current_v=cv.to(device), softmax_scale=scale,
+        return_lse=True, **kw)
+    torch.cuda.synchronize(device)
+    return out, lse
+
+
+def _oracle_schedule(wl):
+    ranges = osched.scale_token_ranges(wl.sides)
+    H, n_prior = wl.keep.shape
+    static = {}
+    for t in range(1, len(wl.sides)):
+        static[t] = {s: {0: {h for h in range(H) if not bool(wl.keep[h, s])}}
+                     for s in range(min(t, n_prior))}
+    pol = osched.PolicyView(static, num_layers=1, source_start=0, source_end=n_prior - 1)
+    return osched.build_schedule(pol, ranges, layer=0, num_heads=H), ranges
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 5])
+def test_slab_pack_bit_exact(cfg, device):
+    wl = W.config(cfg)
+    print(f"[pack] config {cfg} B={wl.batch} H={wl.heads} cap={wl.schedule.capacity}", flush=True)
+    slab_k, slab_v = W.build_slab(wl, device)
+    osch, ranges = _oracle_schedule(wl)
+    assert osch["capacity"] == wl.schedule.capacity
+    st, en, ct = wl.tables()
+    ost, oen, oct_ = osch["metadata_cpu_by_target"][wl.target]
+    assert np.array_equal(st.numpy(), ost) and np.array_equal(en.numpy(), oen)
+    assert np.array_equal(ct.numpy(), oct_)
+    dense_k = torch.cat([wl.prior_k, wl.cur_k], dim=2)
+    dense_v = torch.cat([wl.prior_v, wl.cur_v], dim=2)
+    sk, sv = bits(slab_k), bits(slab_v)
+    owned = np.zeros(wl.schedule.capacity, dtype=bool)
+    for dense, slab in ((dense_k, sk), (dense_v, sv)):
+        exp = opack.expected_live_rows(dense, osch["segments"], wl.target, ranges)
+        for (s, h), (off, rows) in exp.items():
+            n = rows.shape[1]
+            assert np.array_equal(slab[:, off:off + n, :], bits(rows)), (s, h)
+            owned[off:off + n] = True
+    # rows no live segment owns keep the NaN fill (never written)
+    nan_bits = bits(torch.full((1,), float("nan"), dtype=slab_k.dtype))[0]
+    assert (sk[:, ~owned, :] == nan_bits).all()
+
+
+def _check_workload(wl, device, heads=None, batches=None):
+    slab_k, slab_v = W.build_slab(wl, device)
+    out, lse = _run(wl.q, slab_k, slab_v, wl.tables(), wl.cur_k, wl.cur_v, wl.softmax_scale, device)
+    st, en, ct = (t.numpy() for t in wl.tables())
+    osch, _ = _oracle_schedule(wl)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(wl.q), to_np(slab_k), to_np(slab_v), st, en, ct, to_np(wl.cur_k), to_np(wl.cur_v),
+        wl.softmax_scale, heads=heads, batches=batches)
+    o = to_np(out)
+    l = to_np(lse)
+    B, H, L, D = wl.q.shape
+    hs = range(H) if heads is None else heads
+    bs = range(B) if batches is None else batches
+    for b in bs:
+        for h in hs:
+            assert_attention_close(o[b, :, h * D:(h + 1) * D], l[b, h], ref_out[b, :, h * D:(h + 1) * D],
+                                   ref_lse[b, h], what=f"{wl.name} b={b} h={h}")
+
+
+def test_attention_config1(device):
+    print("[attn] config 1", flush=True)
+    _check_workload(W.config(1), device)
+
+
+def test_attention_config2_heads(device):
+    wl = W.config(2)
+    r = wl.retained_rows()
+    order = sorted(range(wl.heads), key=lambda h: r[h])
+    heads = sorted({order[0], order[1], order[-1], order[-2]})
+    print(f"[attn] config 2 heads {heads} R={[r[h] for h in heads]}", flush=True)
+    _check_workload(wl, device, heads=heads, batches=[1])
+
+
+def test_attention_config5_heads(device):
+    wl = W.config(5)
+    r = wl.retained_rows()
+    order = sorted(range(wl.heads), key=lambda h: r[h])
+    heads = sorted({order[0], order[len(order) // 2], order[-1]})
+    print(f"[attn] config 5 heads {heads} R={[r[h] for h in heads]}", flush=True)
+    _check_workload(wl, device, heads=heads, batches=[0, 15])
+
+
+def _random_case(seed, B, H, L, cap, S, *, dtype=torch.bfloat16, kdtype=None, vdtype=None):
+    """Random slab + tables with skipped (start >= end) and unaligned segments."""
+    g = torch.Generator().manual_seed(seed)
+    kdtype = kdtype or dtype
+    vdtype = vdtype or dtype
+    q = torch.randn((B, H, L, 128), generator=g).to(dtype)
+    ck = torch.randn((B, H, L, 128), generator=g).to(kdtype)
+    cv = torch.randn((B, H, L, 128), generator=g).to(vdtype)
+    slab_k = torch.randn((B, cap, 128), generator=g).to(kdtype)
+    slab_v = torch.randn((B, cap, 128), generator=g).to(vdtype)
+    st = torch.zeros((H, S), dtype=torch.int32)
+    en = torch.zeros((H, S), dtype=torch.int32)
+    ct = torch.randint(0, S + 1, (H,), generator=g, dtype=torch.int32)
+    for h in range(H):
+        for i in range(S):
+            a = int(torch.randint(0, cap, (1,), generator=g))
+            n = int(torch.randint(-3, 70, (1,), generator=g))  # n <= 0: skipped entry
+            st[h, i] = a
+            en[h, i] = min(cap, a + n) if n > 0 else a + n
+    return q, slab_k, slab_v, (st, en, ct), ck, cv
+
+
+@pytest.mark.parametrize(
+    "seed,B,H,L,cap,S",
+    [(11, 1, 2, 1, 50, 3), (12, 2, 3, 5, 200, 5), (13, 1, 4, 33, 300, 7), (14, 2, 2, 130, 97, 4),
+     (15, 1, 1, 257, 1000, 12), (16, 3, 5, 64, 0, 0)],
+)
+def test_attention_random_tables(seed, B, H, L, cap, S, device):
+    print(f"[attn] random seed={seed} B={B} H={H} L={L} cap={cap} S={S}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(seed, B, H, L, cap, S)
+    scale = 1.0 / math.sqrt(128)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"seed {seed}")
+
+
+@pytest.mark.parametrize("scale", [-0.3, 0.0, 1.0, 0.02])
+def test_attention_scales(scale, device):
+    print(f"[attn] scale {scale}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(21, 2, 3, 70, 300, 5)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
+    # with scale 1 the scores are O(10), so a bf16-rounded probability weighs
+    # more; the contract tolerance still holds for the output
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"scale {scale}")
+
+
+@pytest.mark.parametrize(
+    "qk,v",
+    [(torch.float16, torch.float16), (torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+     (torch.bfloat16, torch.float16), (torch.float16, torch.bfloat16)],
+)
+def test_attention_dtypes(qk, v, device):
+    print(f"[attn] dtypes qk={qk} v={v}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(31, 2, 2, 90, 400, 6, dtype=qk, kdtype=qk, vdtype=v)
+    scale = 1.0 / math.sqrt(128)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device)
+    assert out.dtype == qk
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
+    # fp32 q/k are rounded to bf16 MFMA operands; the log-sum-exp then moves by
+    # up to ~1e-2 (the output stays within the contract tolerance)
+    lse_tol = 1e-2 if qk == torch.float32 else 1e-3
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, lse_abs=lse_tol,
+                           what=f"{qk}/{v}")
+
+
+def test_attention_no_persisted(device):
+    print("[attn] persisted None", flush=True)
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn((2, 3, 40, 128), generator=g).to(torch.bfloat16) for _ in range(3))
+    tables = (torch.zeros((3, 0), dtype=torch.int32), torch.zeros((3, 0), dtype=torch.int32),
+              torch.zeros((3,), dtype=torch.int32))
+    out, lse = _run(q, None, None, tables, k, v, 0.1, device)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), scale=0.1)
+    ref = ref.transpose(1, 2).reshape(2, 40, 3 * 128)
+    assert_attention_close(to_np(out), None, to_np(ref), None, what="no persisted")
+
+
+@pytest.mark.parametrize("kdt,vdt,D", [(torch.bfloat16, torch.bfloat16, 128), (torch.float32, torch.bfloat16, 128),
+                                       (torch.float16, torch.float32, 64), (torch.bfloat16, torch.bfloat16, 3)])
+def test_pack_random_items(kdt, vdt, D, device):
+    print(f"[pack] random items {kdt} {vdt} D={D}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    B, S_src, cap = 3, 500, 700
+    src_k = torch.randn((B, S_src, D), generator=g).to(kdt)
+    src_v = torch.randn((B, S_src, D), generator=g).to(vdt)
+    dst_k0 = torch.randn((B, cap, D), generator=g).to(kdt)
+    dst_v0 = torch.randn((B, cap, D), generator=g).to(vdt)
+    n_items = 9
+    lengths = torch.randint(0, 90, (n_items,), generator=g)
+    lengths[0] = 0
+    src_starts = torch.stack([torch.randint(0, S_src - int(n) + 1, (1,), generator=g)[0] for n in lengths])
+    # non-overlapping destinations at unaligned offsets
+    dst_starts = torch.cumsum(torch.cat([torch.tensor([3]), lengths[:-1] + 5]), 0)
+    max_len = int(lengths.max())
+    dk, dv = dst_k0.clone().to(device), dst_v0.clone().to(device)
+    pack_flat_segments_kv(dst_k=dk, dst_v=dv, src_k=src_k.to(device), src_v=src_v.to(device),
+                          dst_starts=dst_starts.to(device), src_starts=src_starts.to(device),
+                          lengths=lengths.to(device), max_length=max_len)
+    torch.cuda.synchronize(device)
+    ek = opack.pack_flat_segments(dst_k0.clone(), src_k, dst_starts.tolist(), src_starts.tolist(), lengths.tolist())
+    ev = opack.pack_flat_segments(dst_v0.clone(), src_v, dst_starts.tolist(), src_starts.tolist(), lengths.tolist())
+    assert np.array_equal(bits(dk), bits(ek))
+    assert np.array_equal(bits(dv), bits(ev))
+
+
+def test_pack_max_length_truncates(device):
+    """Items longer than the grid bound copy block_t * ceil(max_length / block_t) rows."""
+    print("[pack] max_length truncation", flush=True)
+    B, D = 1, 128
+    src = torch.arange(B * 200 * D, dtype=torch.float32).reshape(B, 200, D).to(torch.bfloat16)
+    dst = torch.zeros((B, 300, D), dtype=torch.bfloat16)
+    dk, dv = dst.clone().to(device), dst.clone().to(device)
+    meta = [torch.tensor(x, dtype=torch.int64, device=device) for x in ([10], [0], [150])]
+    pack_flat_segments_kv(dst_k=dk, dst_v=dv, src_k=src.to(device), src_v=src.to(device),
+                          dst_starts=meta[0], src_starts=meta[1], lengths=meta[2], max_length=40)
+    torch.cuda.synchronize(device)
+    exp = dst.clone()
+    exp[:, 10:10 + 64] = src[:, :64]  # 32 * ceil(40 / 32) rows
+    assert np.array_equal(bits(dk), bits(exp))
