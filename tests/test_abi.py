@@ -1,0 +1,84 @@
+"""libheatkv.so loads on the host and exports every entry point of include/heatkv.h.
+
+No kernel is launched here (there is no GPU on the build host); only the
+loader functions and the argument checks that fail before any device call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from heatkv_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "heatkv.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(hkv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for n in ("hkv_version", "hkv_device_ok", "hkv_last_error", "hkv_pack_segments",
+              "hkv_segmented_attention"):
+        assert n in names
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libheatkv.so not built")
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True)
+    exported = set(re.findall(r"\sT\s(\w+)$", out.stdout, flags=re.M))
+    for name in _declared():
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_host_only_calls():
+    lib = _lib.load()
+    assert lib.hkv_version() == 0x000100
+    assert lib.hkv_device_ok(-1) == 0
+    assert isinstance(_lib.last_error(), str)
+
+
+def test_argument_errors_before_any_device_call():
+    lib = _lib.load()
+    null = None
+    # head_dim 64 -> unsupported (RuntimeError in Python)
+    code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
+                                       1, 1, 1, 0, 0, 64, 2, 2, 2, ctypes.c_float(1.0), 0, null)
+    assert code == _lib.HKV_ERR_UNSUPPORTED and "head_dim=128" in _lib.last_error()
+    with pytest.raises(RuntimeError, match="head_dim=128"):
+        _lib.check(code)
+    # q/k dtype mismatch
+    code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
+                                       1, 1, 1, 0, 0, 128, 3, 2, 2, ctypes.c_float(1.0), 0, null)
+    assert code == _lib.HKV_ERR_UNSUPPORTED
+    # null pointers -> invalid argument (ValueError)
+    code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
+                                       1, 1, 1, 0, 0, 128, 2, 2, 2, ctypes.c_float(1.0), 0, null)
+    assert code == _lib.HKV_ERR_INVALID_ARG
+    with pytest.raises(ValueError):
+        _lib.check(code)
+    # too many segments
+    code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
+                                       1, 1, 1, 10, 300, 128, 2, 2, 2, ctypes.c_float(1.0), 0, null)
+    assert code == _lib.HKV_ERR_UNSUPPORTED and "max_segments" in _lib.last_error()
+    # pack: empty work is a no-op success, bad head_dim / element size rejected
+    assert lib.hkv_pack_segments(null, null, null, null, 0, 0, 0, 0, 1, 128, 2, 2, null, null, null,
+                                 0, 10, null) == 0
+    assert lib.hkv_pack_segments(null, null, null, null, 0, 0, 0, 0, 1, 256, 2, 2, null, null, null,
+                                 3, 10, null) == _lib.HKV_ERR_UNSUPPORTED
+    assert lib.hkv_pack_segments(null, null, null, null, 0, 0, 0, 0, 1, 128, 8, 2, null, null, null,
+                                 3, 10, null) == _lib.HKV_ERR_UNSUPPORTED
+    assert lib.hkv_pack_segments(null, null, null, null, 0, 0, 0, 0, 1, 128, 2, 2, null, null, null,
+                                 3, 10, null) == _lib.HKV_ERR_INVALID_ARG
