@@ -26,6 +26,9 @@
 //  * Workgroup ids are mapped so that consecutive work items (the query tiles
 //    of one (b, h)) land on the same XCD (dispatch is round-robin over the 8
 //    XCDs) and share that XCD's L2 for the head's K/V stream.
+#include <cstdio>
+#include <cstdlib>
+
 #include "hkv_internal.h"
 
 namespace hkv {
@@ -39,59 +42,65 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;
-constexpr int kBM = 128;                 // queries per workgroup
-constexpr int kBN = 64;                  // keys per tile
-constexpr int kThreads = 256;
-constexpr int kKPitch = kD * 2 + 16;     // bytes per K row in LDS
-constexpr int kVtPitch = kBN * 2;        // bytes per V^T row in LDS
+constexpr int kKPitch = kD * 2 + 16;     // bytes per K row in LDS (16-byte pad: conflict-free reads)
 constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescale: the running max used for exp2 is only moved when a row's max
+// grows by more than this (log2 units); p <= 2^8 stays exact in fp32 and is
+// rounded like any other value to the 16-bit PV operand.
+constexpr float kRescaleLog2 = 8.0f;
+constexpr int kMaxHeads = 1024;
 
 // ---------------------------------------------------------------- conversions
-__device__ __forceinline__ uint32_t pack_bf16(float x, float y) {
-  const uint16_t a = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
-  const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y));
-  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-}
-__device__ __forceinline__ uint32_t pack_f16(float x, float y) {
-  const uint16_t a = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
-  const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(y));
-  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-}
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one dword of two 16-bit values (round to nearest even);
+// the vector conversion lowers to a single v_cvt_pk_{bf16,f16}_f32.
 template <int MT>
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-  if constexpr (MT == kF16) return pack_f16(x, y);
-  else return pack_bf16(x, y);
+  const f32x2_t v = {x, y};
+  if constexpr (MT == kF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t v) {
   return static_cast<float>(__builtin_bit_cast(_Float16, v));
 }
 
-// Loads 8 consecutive elements of type DT at base + elem (elements) and
-// returns them as 8 packed 16-bit values of the MFMA operand type MT.
-// Invalid positions yield zeros (no memory access).
+// Buffer resource over [base, base + bytes): raw loads outside it return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Loads 8 consecutive elements of type DT at byte offset `off` of `r` and
+// returns them as 8 packed 16-bit values of the MFMA operand type MT.  An
+// offset of -1 (outside every resource) yields zeros without a branch.
 template <int DT, int MT>
-__device__ __forceinline__ u32x4_t load8(const void* base, int64_t elem, bool valid) {
-  u32x4_t r = {0u, 0u, 0u, 0u};
-  if (!valid) return r;
+__device__ __forceinline__ u32x4_t load8(__amdgpu_buffer_rsrc_t r, int32_t off) {
   if constexpr (DT == kF32) {
-    const f32x4_t* p = reinterpret_cast<const f32x4_t*>(static_cast<const float*>(base) + elem);
-    const f32x4_t x = p[0];
-    const f32x4_t y = p[1];
-    r[0] = pack2<MT>(x[0], x[1]);
-    r[1] = pack2<MT>(x[2], x[3]);
-    r[2] = pack2<MT>(y[0], y[1]);
-    r[3] = pack2<MT>(y[2], y[3]);
+    // Whole-vector bit casts: casting single elements of a buffer-load result
+    // miscompiles with this toolchain (one dword loaded and replicated).
+    const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    const f32x4_t y = __builtin_bit_cast(
+        f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0));
+    u32x4_t o;
+    o[0] = pack2<MT>(x[0], x[1]);
+    o[1] = pack2<MT>(x[2], x[3]);
+    o[2] = pack2<MT>(y[0], y[1]);
+    o[3] = pack2<MT>(y[2], y[3]);
+    return o;
   } else {
-    r = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(base) + elem);
+    u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     if constexpr (DT == kF16 && MT == kBF16) {
       // fp16 storage feeding a bf16 product (mixed q/k types): widen and round.
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        r[i] = pack_bf16(f16_to_f32(static_cast<uint16_t>(r[i] & 0xffffu)),
-                         f16_to_f32(static_cast<uint16_t>(r[i] >> 16)));
+        v[i] = pack2<kBF16>(f16_to_f32(static_cast<uint16_t>(v[i] & 0xffffu)),
+                            f16_to_f32(static_cast<uint16_t>(v[i] >> 16)));
     }
+    return v;
   }
-  return r;
 }
 
 template <int MT>
@@ -102,13 +111,6 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-
-// Physical 8-byte quad slot of key quad kq in V^T row d.  Distinct over any 16
-// consecutive rows (conflict-free MFMA operand reads) and spread over all 16
-// slots across the 16 d-chunks a wave writes (4-way = minimal write cost).
-__device__ __forceinline__ int vt_slot(int d, int kq) {
-  return kq ^ ((d & 15) ^ ((d >> 4) & 7));
 }
 
 template <int DT>
@@ -123,42 +125,91 @@ __device__ __forceinline__ void store4(void* out, int64_t elem, f32x4_t v) {
   }
 }
 
-template <int QDT, int KDT, int VDT>
-__global__ __launch_bounds__(kThreads, 2) void seg_attn_kernel(AttnArgs a, float c, float scale_abs,
-                                                               uint32_t q_sign, int32_t n_qt) {
+// NW waves per workgroup (32 query rows each), BN keys per tile.
+template <int QDT, int KDT, int VDT, int NW, int BN>
+__global__ __launch_bounds__(NW * 64, (NW == 4 && BN == 128) ? 1 : 2) void seg_attn_kernel(
+    const AttnArgs a, const float c, const float scale_abs, const uint32_t q_sign,
+    const int32_t n_qt) {
   constexpr int MQK = (QDT == kF16 && KDT == kF16) ? kF16 : kBF16;
   constexpr int MV = (VDT == kF16) ? kF16 : kBF16;
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = NW * 32;
+  constexpr int kVtPitch = BN * 2 + 8;      // bytes per V^T row (8-byte pad: conflict-free reads)
+  constexpr int kSB = BN / 32;              // 32-key score blocks per tile
+  constexpr int kQuadChunks = BN / 4 * 16;  // (4-key quad, 16-byte d-chunk) pairs per tensor
+  constexpr int kLoadsPerThread = 2 * kQuadChunks / kThreads;
+  constexpr int kEK = KDT == kF32 ? 4 : 2;  // element bytes
+  constexpr int kEV = VDT == kF32 ? 4 : 2;
+  constexpr int kEQ = QDT == kF32 ? 4 : 2;
+  static_assert(2 * kQuadChunks % kThreads == 0, "loader split");
 
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[kBN * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[BN * kKPitch];
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kD * kVtPitch];
-  __shared__ __attribute__((aligned(16))) int32_t rowtab[2][kBN];
+  __shared__ __attribute__((aligned(16))) int32_t rowtab[2][BN];
   __shared__ int32_t seg_start[kMaxSegments];
   __shared__ int32_t seg_pref[kMaxSegments + 1];
+  __shared__ int32_t head_rows[kMaxHeads];
+  __shared__ int32_t head_by_rank[kMaxHeads];
+
+  // Kernel arguments copied to locals once (keeps them in SGPRs).
+  const int32_t* __restrict__ seg_starts = a.seg_starts;
+  const int32_t* __restrict__ seg_ends = a.seg_ends;
+  const int32_t* __restrict__ seg_counts = a.seg_counts;
+  const int64_t cap = a.slab_capacity;
+  const int H = a.heads;
+  const int L = a.cur_len;
+  const int S = a.max_segments;
+  const int B = a.batch;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int g = lane >> 5;  // half of the wave: selects the k-slot group of MFMA operands
-  const int H = a.heads;
-  const int L = a.cur_len;
 
-  // ---- work item (XCD-aware: equal shares of consecutive items per XCD)
-  const int32_t n_items = a.batch * H * n_qt;
-  int32_t item = blockIdx.x;
-  if ((n_items & 7) == 0) item = (blockIdx.x & 7) * (n_items >> 3) + (blockIdx.x >> 3);
-  const int32_t bh = item / n_qt;
-  const int32_t qt = item - bh * n_qt;
-  const int32_t b = bh / H;
-  const int32_t h = bh - b * H;
+  // ---- longest-first order of heads: every head's retained rows, then ranks
+  for (int hh = tid; hh < H; hh += kThreads) {
+    int n = seg_counts[hh];
+    n = n < 0 ? 0 : (n > S ? S : n);
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+      int64_t st = seg_starts[static_cast<int64_t>(hh) * S + i];
+      int64_t en = seg_ends[static_cast<int64_t>(hh) * S + i];
+      st = st < 0 ? 0 : (st > cap ? cap : st);
+      en = en < 0 ? 0 : (en > cap ? cap : en);
+      rows += en > st ? en - st : 0;
+    }
+    head_rows[hh] = static_cast<int32_t>(rows);
+  }
+  __syncthreads();
+  for (int hh = tid; hh < H; hh += kThreads) {
+    const int r = head_rows[hh];
+    int rank = 0;
+    for (int o = 0; o < H; ++o) {
+      const int ro = head_rows[o];
+      rank += (ro > r) || (ro == r && o < hh);
+    }
+    head_by_rank[rank] = hh;
+  }
+  __syncthreads();
+
+  // ---- work item: heaviest heads first (workgroups start in id order, so the
+  // dispatcher's greedy slot filling approximates longest-processing-time)
+  const int32_t per_rank = B * n_qt;
+  const int32_t rank = blockIdx.x / per_rank;
+  const int32_t rem = blockIdx.x - rank * per_rank;
+  const int32_t b = rem / n_qt;
+  const int32_t qt = rem - b * n_qt;
+  const int32_t h = head_by_rank[rank];
+  const int32_t bh = b * H + h;
 
   // ---- segment table of head h: clamped starts and exclusive length prefix
-  int nseg = a.seg_counts[h];
-  nseg = nseg < 0 ? 0 : (nseg > a.max_segments ? a.max_segments : nseg);
+  int nseg = seg_counts[h];
+  nseg = nseg < 0 ? 0 : (nseg > S ? S : nseg);
   for (int i = tid; i < nseg; i += kThreads) {
-    int64_t st = a.seg_starts[static_cast<int64_t>(h) * a.max_segments + i];
-    int64_t en = a.seg_ends[static_cast<int64_t>(h) * a.max_segments + i];
-    st = st < 0 ? 0 : (st > a.slab_capacity ? a.slab_capacity : st);
-    en = en < 0 ? 0 : (en > a.slab_capacity ? a.slab_capacity : en);
+    int64_t st = seg_starts[static_cast<int64_t>(h) * S + i];
+    int64_t en = seg_ends[static_cast<int64_t>(h) * S + i];
+    st = st < 0 ? 0 : (st > cap ? cap : st);
+    en = en < 0 ? 0 : (en > cap ? cap : en);
     seg_start[i] = static_cast<int32_t>(st);
     seg_pref[i + 1] = en > st ? static_cast<int32_t>(en - st) : 0;
   }
@@ -188,65 +239,113 @@ __global__ __launch_bounds__(kThreads, 2) void seg_attn_kernel(AttnArgs a, float
     if (lane == 0) seg_pref[0] = 0;
   }
   __syncthreads();
-  const int32_t R = seg_pref[nseg];  // retained prior rows of this head
-  const int32_t T = R + L;           // keys in the stream
-  const int32_t ntiles = (T + kBN - 1) / kBN;
+  // Key stream: ntp tiles of retained prior rows (the last one padded), then
+  // ntc tiles of current rows; every tile reads one tensor only.
+  const int32_t R = seg_pref[nseg];
+  const int32_t ntp = (R + BN - 1) / BN;
+  const int32_t ntc = (L + BN - 1) / BN;
+  const int32_t ntiles = ntp + ntc;
 
-  // ---- row table: stream position -> slab row (>= 0) or ~current row (< 0)
+  // Buffer resources: batch b's slab rows and (b, h)'s current rows.
+  const __amdgpu_buffer_rsrc_t rs_k = make_rsrc(
+      static_cast<const uint8_t*>(a.slab_k) + static_cast<int64_t>(b) * cap * kD * kEK,
+      static_cast<uint32_t>(cap * kD * kEK));
+  const __amdgpu_buffer_rsrc_t rs_v = make_rsrc(
+      static_cast<const uint8_t*>(a.slab_v) + static_cast<int64_t>(b) * cap * kD * kEV,
+      static_cast<uint32_t>(cap * kD * kEV));
+  const int64_t cur_row0 = static_cast<int64_t>(bh) * L;
+  const __amdgpu_buffer_rsrc_t rc_k = make_rsrc(
+      static_cast<const uint8_t*>(a.cur_k) + cur_row0 * kD * kEK, static_cast<uint32_t>(L * kD * kEK));
+  const __amdgpu_buffer_rsrc_t rc_v = make_rsrc(
+      static_cast<const uint8_t*>(a.cur_v) + cur_row0 * kD * kEV, static_cast<uint32_t>(L * kD * kEV));
+
+  // ---- row table of a prior tile: stream position -> slab row, -1 past R
   int cur_seg = 0;
   auto fill_rowtab = [&](int tile, int buf) {
-    const int j0 = tile * kBN;
+    const int j0 = tile * BN;
     while (cur_seg < nseg && seg_pref[cur_seg + 1] <= j0) ++cur_seg;
-    const int j = j0 + lane;
-    int code;
-    if (j < R) {
-      int s = cur_seg;
-      while (seg_pref[s + 1] <= j) ++s;
-      code = seg_start[s] + (j - seg_pref[s]);
-    } else if (j < T) {
-      code = ~(j - R);
-    } else {
-      code = ~0;  // never dereferenced: loads of keys >= T are skipped
+#pragma unroll
+    for (int part = 0; part < BN / 64; ++part) {
+      const int j = j0 + part * 64 + lane;
+      int row = -1;
+      if (j < R) {
+        int s = cur_seg;
+        while (seg_pref[s + 1] <= j) ++s;
+        row = seg_start[s] + (j - seg_pref[s]);
+      }
+      rowtab[buf][part * 64 + lane] = row;
     }
-    rowtab[buf][lane] = code;
   };
 
-  // ---- loader role: key quad lq (keys 4lq..4lq+3), d-chunk lc (d 8lc..8lc+7)
-  const int lq = tid >> 4;
-  const int lc = tid & 15;
-  u32x4_t kreg[4];
-  u32x4_t vreg[4];
-  const int64_t slab_row0 = static_cast<int64_t>(b) * a.slab_capacity;
-  const int64_t cur_row0 = static_cast<int64_t>(bh) * L;
+  // ---- loader: quad-chunk i covers keys 4(i/16)..+3 at d 8(i%16)..+7 of K (i <
+  // kQuadChunks) or of V; thread tid owns quad-chunks tid, tid + kThreads, ...
+  u32x4_t lreg[kLoadsPerThread][4];
   auto issue_loads = [&](int tile, int buf) {
-    const int4 codes = *reinterpret_cast<const int4*>(&rowtab[buf][lq * 4]);
-    const int cc[4] = {codes.x, codes.y, codes.z, codes.w};
+    if (tile < ntp) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int code = cc[i];
-      const bool valid = tile * kBN + lq * 4 + i < T;
-      const bool in_slab = code >= 0;
-      const int64_t row = in_slab ? slab_row0 + code : cur_row0 + (~code);
-      const int64_t elem = row * kD + lc * 8;
-      kreg[i] = load8<KDT, MQK>(in_slab ? a.slab_k : a.cur_k, elem, valid);
-      vreg[i] = load8<VDT, MV>(in_slab ? a.slab_v : a.cur_v, elem, valid);
+      for (int it = 0; it < kLoadsPerThread; ++it) {
+        const int item = tid + it * kThreads;
+        const bool is_v = item >= kQuadChunks;
+        const int qc = is_v ? item - kQuadChunks : item;
+        const int lq = qc >> 4;
+        const int lc = qc & 15;
+        const int4 rows = *reinterpret_cast<const int4*>(&rowtab[buf][lq * 4]);
+        const int rr[4] = {rows.x, rows.y, rows.z, rows.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (is_v)
+            lreg[it][i] = load8<VDT, MV>(rs_v, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEV);
+          else
+            lreg[it][i] = load8<KDT, MQK>(rs_k, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEK);
+        }
+      }
+    } else {
+      const int row0 = (tile - ntp) * BN;
+#pragma unroll
+      for (int it = 0; it < kLoadsPerThread; ++it) {
+        const int item = tid + it * kThreads;
+        const bool is_v = item >= kQuadChunks;
+        const int qc = is_v ? item - kQuadChunks : item;
+        const int lq = qc >> 4;
+        const int lc = qc & 15;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + lq * 4 + i;
+          if (is_v)
+            lreg[it][i] = load8<VDT, MV>(rc_v, row < L ? (row * kD + lc * 8) * kEV : -1);
+          else
+            lreg[it][i] = load8<KDT, MQK>(rc_k, row < L ? (row * kD + lc * 8) * kEK : -1);
+        }
+      }
     }
   };
   auto store_tile = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4_t*>(k_lds + (lq * 4 + i) * kKPitch + lc * 16) = kreg[i];
+    for (int it = 0; it < kLoadsPerThread; ++it) {
+      const int item = tid + it * kThreads;
+      const bool is_v = item >= kQuadChunks;
+      const int qc = is_v ? item - kQuadChunks : item;
+      const int lq = qc >> 4;
+      const int lc = qc & 15;
+      const u32x4_t* r = lreg[it];
+      if (!is_v) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      u32x2_t even, odd;
-      even[0] = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], 0x05040100u);
-      even[1] = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], 0x05040100u);
-      odd[0] = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], 0x07060302u);
-      odd[1] = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], 0x07060302u);
-      const int d0 = lc * 8 + 2 * w;
-      const int d1 = d0 + 1;
-      *reinterpret_cast<u32x2_t*>(vt_lds + d0 * kVtPitch + 8 * vt_slot(d0, lq)) = even;
-      *reinterpret_cast<u32x2_t*>(vt_lds + d1 * kVtPitch + 8 * vt_slot(d1, lq)) = odd;
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<u32x4_t*>(k_lds + (lq * 4 + i) * kKPitch + lc * 16) = r[i];
+      } else {
+        // transpose 4 keys x 8 d into 8 rows of V^T (4 keys each)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          u32x2_t even, odd;
+          even[0] = __builtin_amdgcn_perm(r[1][w], r[0][w], 0x05040100u);
+          even[1] = __builtin_amdgcn_perm(r[3][w], r[2][w], 0x05040100u);
+          odd[0] = __builtin_amdgcn_perm(r[1][w], r[0][w], 0x07060302u);
+          odd[1] = __builtin_amdgcn_perm(r[3][w], r[2][w], 0x07060302u);
+          uint8_t* row = vt_lds + (lc * 8 + 2 * w) * kVtPitch + lq * 8;
+          *reinterpret_cast<u32x2_t*>(row) = even;
+          *reinterpret_cast<u32x2_t*>(row + kVtPitch) = odd;
+        }
+      }
     }
   };
 
@@ -254,88 +353,98 @@ __global__ __launch_bounds__(kThreads, 2) void seg_attn_kernel(AttnArgs a, float
   const int32_t qrow = qt * kBM + wave * 32 + (lane & 31);
   const bool qvalid = qrow < L;
   u32x4_t qf[8];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * kEQ, static_cast<uint32_t>(L * kD * kEQ));
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    qf[ks] = load8<QDT, MQK>(a.q, (cur_row0 + qrow) * kD + ks * 16 + g * 8, qvalid);
-    qf[ks] ^= q_sign;  // negative softmax scale: exact sign flip of q
+    for (int ks = 0; ks < 8; ++ks) {
+      qf[ks] = load8<QDT, MQK>(rq, qvalid ? (qrow * kD + ks * 16 + g * 8) * kEQ : -1);
+      qf[ks] ^= q_sign;  // negative softmax scale: exact sign flip of q
+    }
   }
 
   f32x16_t oacc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
-  float m_run = -1e30f;  // running max of raw scores (sign-adjusted)
+  float m_run = -1e30f;  // reference max of raw scores (sign-adjusted) used by exp2
   float l_run = 0.f;     // this lane's partial row sum
+  const float thresh = c > 0.f ? kRescaleLog2 / c : 0.f;
 
-  if (wave == 0) fill_rowtab(0, 0);
+  // LDS operand addresses: lane part here, the rest are immediates.
+  const uint8_t* k_lane = k_lds + (lane & 31) * kKPitch + g * 16;
+  const uint8_t* v_lane = vt_lds + (lane & 31) * kVtPitch + g * 8;
+
+  if (wave == 0 && ntp > 0) fill_rowtab(0, 0);
   __syncthreads();
   issue_loads(0, 0);
-  if (wave == 0 && ntiles > 1) fill_rowtab(1, 1);
+  if (wave == 0 && 1 < ntp) fill_rowtab(1, 1);
 
   for (int t = 0; t < ntiles; ++t) {
     store_tile();
     __syncthreads();
     if (t + 1 < ntiles) issue_loads(t + 1, (t + 1) & 1);
-    if (wave == 0 && t + 2 < ntiles) fill_rowtab(t + 2, t & 1);
+    if (wave == 0 && t + 2 < ntp) fill_rowtab(t + 2, t & 1);
 
     // S^T block kb: keys 32kb + (8(j>>2) + 4g + (j&3)), query lane&31
-    f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+    f32x16_t s[kSB];
+#pragma unroll
+    for (int kb = 0; kb < kSB; ++kb) s[kb] = f32x16_t{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(
-            k_lds + (kb * 32 + (lane & 31)) * kKPitch + (ks * 16 + g * 8) * 2);
+      for (int kb = 0; kb < kSB; ++kb) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lane + kb * 32 * kKPitch + ks * 32);
         s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
       }
     }
-    const bool tail = (t + 1) * kBN > T;
-    if (tail) {
+    // keys of this tile that exist: prior tiles end at R, current tiles at L
+    const int valid_keys = t < ntp ? min(BN, R - t * BN) : min(BN, L - (t - ntp) * BN);
+    const bool partial = valid_keys < BN;
+    if (partial) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < kSB; ++kb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = t * kBN + kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-          if (key >= T) s[kb][j] = -__builtin_inff();
-        }
+        for (int j = 0; j < 16; ++j)
+          if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = -__builtin_inff();
     }
     float mx = s[0][0];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < kSB; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f((m_run - m_new) * c);
-    const float mc = m_new * c;
+    // Move the reference max only when some row of the wave grew past the
+    // threshold (always on the first tile, where m_run is -1e30).
+    if (__any(mx - m_run > thresh)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run * c;
+#pragma unroll
+    for (int kb = 0; kb < kSB; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[kb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c, -mc));
+    if (partial) {
+#pragma unroll
+      for (int kb = 0; kb < kSB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = 0.f;
+    }
     float psum = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float p = exp2f(__builtin_fmaf(s[kb][j], c, -mc));
-        s[kb][j] = p;
-      }
-    if (tail) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = t * kBN + kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-          if (key >= T) s[kb][j] = 0.f;
-        }
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < kSB; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) psum += s[kb][j];
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    l_run += psum;
 
     // O^T += V^T P^T: k-step u covers keys 16u + {4g..4g+3, 8+4g..8+4g+3}
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < BN / 16; ++u) {
       const f32x16_t& sp = s[u >> 1];
       const int j0 = 8 * (u & 1);
       u32x4_t pf;
@@ -345,10 +454,9 @@ __global__ __launch_bounds__(kThreads, 2) void seg_attn_kernel(AttnArgs a, float
       pf[3] = pack2<MV>(sp[j0 + 6], sp[j0 + 7]);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int d = db * 32 + (lane & 31);
-        const uint8_t* row = vt_lds + d * kVtPitch;
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row + 8 * vt_slot(d, 4 * u + g));
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 8 * vt_slot(d, 4 * u + 2 + g));
+        const uint8_t* row = v_lane + db * 32 * kVtPitch + 32 * u;
+        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
+        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 16);
         u32x4_t vf;
         vf[0] = lo[0];
         vf[1] = lo[1];
@@ -382,34 +490,68 @@ __global__ __launch_bounds__(kThreads, 2) void seg_attn_kernel(AttnArgs a, float
   }
 }
 
+struct Variant {
+  int nw;
+  int bn;
+};
+
+// Tile shape: waves per workgroup x keys per tile.  HKV_ATTN_VARIANT (read
+// once) selects another compiled shape for tuning sweeps: "4x64", "8x64",
+// "4x128" (one wave per SIMD, accumulators in AGPRs).
+Variant variant() {
+  static Variant v = [] {
+    Variant r{4, 64};
+    if (const char* e = std::getenv("HKV_ATTN_VARIANT")) {
+      int nw = 0, bn = 0;
+      if (std::sscanf(e, "%dx%d", &nw, &bn) == 2 &&
+          ((nw == 4 && (bn == 64 || bn == 128)) || (nw == 8 && bn == 64)))
+        r = Variant{nw, bn};
+    }
+    return r;
+  }();
+  return v;
+}
+
+template <int QDT, int KDT, int VDT>
+hipError_t launch_shape(const AttnArgs& a, float c, float sabs, uint32_t qs, hipStream_t st) {
+  const Variant v = variant();
+  const int32_t bm = v.nw * 32;
+  const int32_t n_qt = (a.cur_len + bm - 1) / bm;
+  const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  if (v.nw == 4 && v.bn == 64)
+    seg_attn_kernel<QDT, KDT, VDT, 4, 64><<<grid, 256, 0, st>>>(a, c, sabs, qs, n_qt);
+  else if (v.nw == 8 && v.bn == 64)
+    seg_attn_kernel<QDT, KDT, VDT, 8, 64><<<grid, 512, 0, st>>>(a, c, sabs, qs, n_qt);
+  else
+    seg_attn_kernel<QDT, KDT, VDT, 4, 128><<<grid, 256, 0, st>>>(a, c, sabs, qs, n_qt);
+  return hipGetLastError();
+}
+
 template <int QDT, int KDT>
-hipError_t dispatch_v(const AttnArgs& a, dim3 grid, float c, float sabs, uint32_t qs, int32_t nqt,
-                      hipStream_t st) {
+hipError_t dispatch_v(const AttnArgs& a, float c, float sabs, uint32_t qs, hipStream_t st) {
   switch (a.v_dtype) {
-    case kBF16: seg_attn_kernel<QDT, KDT, kBF16><<<grid, kThreads, 0, st>>>(a, c, sabs, qs, nqt); break;
-    case kF16: seg_attn_kernel<QDT, KDT, kF16><<<grid, kThreads, 0, st>>>(a, c, sabs, qs, nqt); break;
-    case kF32: seg_attn_kernel<QDT, KDT, kF32><<<grid, kThreads, 0, st>>>(a, c, sabs, qs, nqt); break;
+    case kBF16: return launch_shape<QDT, KDT, kBF16>(a, c, sabs, qs, st);
+    case kF16: return launch_shape<QDT, KDT, kF16>(a, c, sabs, qs, st);
+    case kF32: return launch_shape<QDT, KDT, kF32>(a, c, sabs, qs, st);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream) {
-  const int32_t n_qt = (a.cur_len + kBM - 1) / kBM;
-  const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
-  if (blocks <= 0) return hipSuccess;
-  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  dim3 grid(static_cast<uint32_t>(blocks));
+  if (a.heads > kMaxHeads) return hipErrorInvalidValue;
   const float sabs = a.softmax_scale < 0.f ? -a.softmax_scale : a.softmax_scale;
   const float c = sabs * kLog2e;
   const uint32_t qs = a.softmax_scale < 0.f ? 0x80008000u : 0u;
   if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
   switch (a.q_dtype) {
-    case kBF16: return dispatch_v<kBF16, kBF16>(a, grid, c, sabs, qs, n_qt, stream);
-    case kF16: return dispatch_v<kF16, kF16>(a, grid, c, sabs, qs, n_qt, stream);
-    case kF32: return dispatch_v<kF32, kF32>(a, grid, c, sabs, qs, n_qt, stream);
+    case kBF16: return dispatch_v<kBF16, kBF16>(a, c, sabs, qs, stream);
+    case kF16: return dispatch_v<kF16, kF16>(a, c, sabs, qs, stream);
+    case kF32: return dispatch_v<kF32, kF32>(a, c, sabs, qs, stream);
     default: return hipErrorInvalidValue;
   }
 }
