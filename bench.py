@@ -76,7 +76,13 @@ def time_attention(wl, device, steps, warmup):
         b.record(stream)
     torch.cuda.synchronize(device)
     kern = [a.elapsed_time(b) for a, b in evs]
-    return ms_per_step, statistics.mean(kern), statistics.median(kern)
+    # (3) host cost of one call (enqueue only; the GPU is left to drain)
+    t_host = time.perf_counter()
+    for _ in range(steps):
+        fused_real_pruning_flat_segmented_attention(**kw)
+    host_us = (time.perf_counter() - t_host) / steps * 1e6
+    torch.cuda.synchronize(device)
+    return ms_per_step, statistics.mean(kern), statistics.median(kern), host_us
 
 
 def time_pack(wl, device, reps=20):
@@ -164,7 +170,7 @@ def main():
     device = torch.device("cuda:0")
     wl = W.config(args.config, budget=args.budget)
     flops = wl.attention_flops()
-    ms_step, kern_mean, kern_med = time_attention(wl, device, args.steps, args.warmup)
+    ms_step, kern_mean, kern_med, host_us = time_attention(wl, device, args.steps, args.warmup)
     achieved = flops / (kern_mean * 1e-3)
     pack_ms, pack_bytes, pack_calls = time_pack(wl, device)
     rec = {
@@ -193,6 +199,7 @@ def main():
             "kernel": "seg_attn_kernel", "kernel_ms_mean": round(kern_mean, 5),
             "kernel_ms_median": round(kern_med, 5),
         },
+        "host_us_per_call": round(host_us, 1),
         "compaction": {
             "what": f"slab fill: {pack_calls} append launches (every kept prior scale)",
             "ms": round(pack_ms, 5), "bytes": pack_bytes,

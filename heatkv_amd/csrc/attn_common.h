@@ -1,0 +1,339 @@
+// Device pieces shared by the two segmented-attention kernels
+// (seg_attn_direct.hip for 16-bit K/V, seg_attn_staged.hip for fp32 K or V).
+//
+// Semantics follow _fused_real_pruning_segmented_attention_kernel
+// (real_pruning_fused_attention.py:76-267): query l of (b, h) attends to the
+// slab rows of head h's segments in table order, then to the current scale's
+// K/V rows of (b, h); online softmax with fp32 statistics, P rounded to the V
+// operand type before the PV product, O / l at the end, output [B, L, H*D].
+//
+// Common structure of both kernels (CDNA4, wave64):
+//  * A workgroup handles 32 * NW queries of one (b, h); each wave owns 32
+//    query rows and keeps their Q fragments in registers.
+//  * Keys are walked as a stream of 64-key tiles: the retained prior rows of
+//    head h (all segments back to back, no per-segment tile restart; a row
+//    table maps stream position -> slab row) then, starting on a fresh tile,
+//    the current rows.  Every tile therefore reads one tensor only.
+//  * S^T = K Q^T on v_mfma_f32_32x32x16_{bf16,f16}: keys are the M index, so
+//    each lane holds one query's scores (16 per 32-key block); row max and sum
+//    need one exchange between lanes l and l + 32, and the fp32 scores convert
+//    in place to the B operand of O^T = V^T P^T.
+//  * exp2 with scale * log2(e) folded into one FMA per score; the running max
+//    is moved lazily (only when a row grows by more than 2^8).
+//  * Work items are ordered heaviest head first (longest-processing-time
+//    order); the dispatcher fills free CU slots in workgroup-id order.
+#pragma once
+
+#include "hkv_internal.h"
+
+namespace hkv {
+namespace attn {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kD = 128;
+constexpr int kBN = 64;  // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescale: the reference max used by exp2 moves only when a row's max
+// grows by more than this (log2 units); p <= 2^8 stays exact in fp32 and is
+// rounded like any other value to the 16-bit PV operand.
+constexpr float kRescaleLog2 = 8.0f;
+constexpr int kMaxHeads = 1024;
+
+// ---------------------------------------------------------------- conversions
+
+// Two fp32 values -> one dword of two 16-bit values (round to nearest even);
+// the vector conversion lowers to a single v_cvt_pk_{bf16,f16}_f32.
+template <int MT>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  const f32x2_t v = {x, y};
+  if constexpr (MT == kF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+// Buffer resource over [base, base + bytes): raw loads outside it return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// Loads 8 consecutive elements of type DT at byte offset `off` of `r` and
+// returns them as 8 packed 16-bit values of the MFMA operand type MT.  An
+// offset of -1 (outside every resource) yields zeros without a branch.
+template <int DT, int MT>
+__device__ __forceinline__ u32x4_t load8(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  if constexpr (DT == kF32) {
+    // Whole-vector bit casts: casting single elements of a buffer-load result
+    // miscompiles with this toolchain (one dword loaded and replicated).
+    const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    const f32x4_t y = __builtin_bit_cast(
+        f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0));
+    u32x4_t o;
+    o[0] = pack2<MT>(x[0], x[1]);
+    o[1] = pack2<MT>(x[2], x[3]);
+    o[2] = pack2<MT>(y[0], y[1]);
+    o[3] = pack2<MT>(y[2], y[3]);
+    return o;
+  } else {
+    u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    if constexpr (DT == kF16 && MT == kBF16) {
+      // fp16 storage feeding a bf16 product (mixed q/k types): widen and round.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = pack2<kBF16>(f16_to_f32(static_cast<uint16_t>(v[i] & 0xffffu)),
+                            f16_to_f32(static_cast<uint16_t>(v[i] >> 16)));
+    }
+    return v;
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (MT == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ void store4(void* out, int64_t elem, f32x4_t v) {
+  if constexpr (DT == kF32) {
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(out) + elem) = v;
+  } else {
+    u32x2_t w;
+    w[0] = pack2<DT>(v[0], v[1]);
+    w[1] = pack2<DT>(v[2], v[3]);
+    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(out) + elem) = w;
+  }
+}
+
+// ---------------------------------------------------------------- work plan
+
+struct WorkItem {
+  int32_t b, h, qt, bh;
+  int32_t nseg;  // live segment entries of head h
+  int32_t R;     // retained prior rows of head h
+};
+
+// Longest-first order of the heads, this workgroup's (b, h, query tile), and
+// head h's clamped segment starts + exclusive length prefix in LDS.  Ends
+// with a workgroup barrier.  head_rows / head_by_rank need `heads` entries.
+template <int kThreads>
+__device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_starts,
+                                              const int32_t* __restrict__ seg_ends,
+                                              const int32_t* __restrict__ seg_counts, int64_t cap,
+                                              int H, int S, int B, int32_t n_qt,
+                                              int32_t* head_rows, int32_t* head_by_rank,
+                                              int32_t* seg_start, int32_t* seg_pref) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int hh = tid; hh < H; hh += kThreads) {
+    int n = seg_counts[hh];
+    n = n < 0 ? 0 : (n > S ? S : n);
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+      int64_t st = seg_starts[static_cast<int64_t>(hh) * S + i];
+      int64_t en = seg_ends[static_cast<int64_t>(hh) * S + i];
+      st = st < 0 ? 0 : (st > cap ? cap : st);
+      en = en < 0 ? 0 : (en > cap ? cap : en);
+      rows += en > st ? en - st : 0;
+    }
+    head_rows[hh] = static_cast<int32_t>(rows);
+  }
+  __syncthreads();
+  for (int hh = tid; hh < H; hh += kThreads) {
+    const int r = head_rows[hh];
+    int rank = 0;
+    for (int o = 0; o < H; ++o) {
+      const int ro = head_rows[o];
+      rank += (ro > r) || (ro == r && o < hh);
+    }
+    head_by_rank[rank] = hh;
+  }
+  __syncthreads();
+
+  WorkItem w;
+  const int32_t per_rank = B * n_qt;
+  const int32_t rank = blockIdx.x / per_rank;
+  const int32_t rem = blockIdx.x - rank * per_rank;
+  w.b = rem / n_qt;
+  w.qt = rem - w.b * n_qt;
+  w.h = head_by_rank[rank];
+  w.bh = w.b * H + w.h;
+
+  int nseg = seg_counts[w.h];
+  nseg = nseg < 0 ? 0 : (nseg > S ? S : nseg);
+  for (int i = tid; i < nseg; i += kThreads) {
+    int64_t st = seg_starts[static_cast<int64_t>(w.h) * S + i];
+    int64_t en = seg_ends[static_cast<int64_t>(w.h) * S + i];
+    st = st < 0 ? 0 : (st > cap ? cap : st);
+    en = en < 0 ? 0 : (en > cap ? cap : en);
+    seg_start[i] = static_cast<int32_t>(st);
+    seg_pref[i + 1] = en > st ? static_cast<int32_t>(en - st) : 0;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int v[4];
+    int local = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = lane * 4 + k;
+      v[k] = idx < nseg ? seg_pref[idx + 1] : 0;
+      local += v[k];
+    }
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = lane * 4 + k;
+      run += v[k];
+      if (idx < nseg) seg_pref[idx + 1] = run;
+    }
+    if (lane == 0) seg_pref[0] = 0;
+  }
+  __syncthreads();
+  w.nseg = nseg;
+  w.R = seg_pref[nseg];
+  return w;
+}
+
+// Row table of prior tile `tile` (wave 0, one entry per lane per 64 keys):
+// stream position -> slab row, or -1 past R.  `cur_seg` walks forward with the
+// tiles (callers fill tiles in increasing order).
+__device__ __forceinline__ void fill_rowtab(int tile, int32_t* rowtab, int& cur_seg, int nseg, int R,
+                                            const int32_t* seg_start, const int32_t* seg_pref) {
+  const int lane = threadIdx.x & 63;
+  const int j0 = tile * kBN;
+  while (cur_seg < nseg && seg_pref[cur_seg + 1] <= j0) ++cur_seg;
+  const int j = j0 + lane;
+  int row = -1;
+  if (j < R) {
+    int s = cur_seg;
+    while (seg_pref[s + 1] <= j) ++s;
+    row = seg_start[s] + (j - seg_pref[s]);
+  }
+  rowtab[lane] = row;
+}
+
+// ---------------------------------------------------------------- softmax
+
+// Online softmax of one 64-key tile held as S^T blocks (keys 32kb + 8(j>>2) +
+// 4g + (j&3), query = lane & 31).  Overwrites s with p = exp2(c (s - m)) (0 for
+// keys >= valid_keys), rescales oacc / l_run when the reference max moves.
+__device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[4], float& m_run,
+                                             float& l_run, float c, float thresh, int valid_keys,
+                                             int g) {
+  const bool partial = valid_keys < kBN;
+  if (partial) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = -__builtin_inff();
+  }
+  float mx = s[0][0];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (__any(mx - m_run > thresh)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    m_run = m_new;
+  }
+  const float mc = m_run * c;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s[kb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c, -mc));
+  if (partial) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = 0.f;
+  }
+  float psum = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) psum += s[kb][j];
+  l_run += psum;
+}
+
+// P^T B-operand for PV k-step u (keys 16u + {4g..4g+3, 8+4g..8+4g+3}).
+template <int MV>
+__device__ __forceinline__ u32x4_t p_operand(const f32x16_t (&s)[2], int u) {
+  const f32x16_t& sp = s[u >> 1];
+  const int j0 = 8 * (u & 1);
+  u32x4_t pf;
+  pf[0] = pack2<MV>(sp[j0 + 0], sp[j0 + 1]);
+  pf[1] = pack2<MV>(sp[j0 + 2], sp[j0 + 3]);
+  pf[2] = pack2<MV>(sp[j0 + 4], sp[j0 + 5]);
+  pf[3] = pack2<MV>(sp[j0 + 6], sp[j0 + 7]);
+  return pf;
+}
+
+// O = acc / l to out[b, q, h*D + d] (d = 32db + 8(j>>2) + 4g + (j&3)), and
+// lse = scale * m + ln(l) for the lane's query.
+template <int QDT>
+__device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_run, float l_run,
+                                             float scale_abs, void* out, float* lse, int64_t b,
+                                             int64_t h, int32_t qrow, int L, int H, int64_t bh,
+                                             int g) {
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.f / l_tot;
+  if (qrow >= L) return;
+  const int64_t out_row = (b * L + qrow) * (static_cast<int64_t>(H) * kD) + h * kD;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      f32x4_t v;
+      v[0] = oacc[db][4 * jb + 0] * inv;
+      v[1] = oacc[db][4 * jb + 1] * inv;
+      v[2] = oacc[db][4 * jb + 2] * inv;
+      v[3] = oacc[db][4 * jb + 3] * inv;
+      store4<QDT>(out, out_row + db * 32 + 8 * jb + 4 * g, v);
+    }
+  if (lse != nullptr && g == 0) lse[bh * L + qrow] = m_run * scale_abs + __logf(l_tot);
+}
+
+// Launch plumbing shared by the two kernels.
+struct Scalars {
+  float c;          // |scale| * log2(e)
+  float scale_abs;  // |scale|
+  uint32_t q_sign;  // 0x80008000 when scale < 0: q's 16-bit operands are negated
+};
+
+}  // namespace attn
+
+hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);
+hipError_t launch_attention_staged(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);
+bool attention_direct_supported(const AttnArgs& a);
+
+}  // namespace hkv

@@ -1,0 +1,295 @@
+// Segmented attention, direct-to-LDS variant for 16-bit K and V (bf16/fp16).
+//
+// K/V tiles move global -> LDS with buffer_load_dwordx4 ... lds (asynchronous,
+// no register staging; rows outside the tensors arrive as zeros) into a ring
+// of NS stages, NS - 1 tiles ahead of the compute, with one barrier per tile.
+//
+// LDS holds each tile in MFMA-operand order, so every operand read is one
+// contiguous 1 KiB (K) or 512 B (V) block per wave at a constant offset:
+//  * K block (kb, ks), 1 KiB: lane l's 16 bytes are K[32kb + l%32][16ks +
+//    8(l/32) .. +7], the A operand of S^T = K Q^T.  One DMA instruction fills
+//    one block (32 key rows x 32 bytes).
+//  * V block (db, u, h), 512 B: 64 chunks of 4 values; chunk 16G + j holds
+//    V[16u + 4(G/2) + 8h + j/4][32db + 16(G%2) + 4(j%4) .. +3].  ds_read_b64_
+//    tr_b16 of lane l at chunk l then yields V[16u + 4g + 8h + m][32db + l%32]
+//    for m = 0..3 (lane i of a 16-lane group receives element i%4 of the
+//    chunks of lanes 4m + i/4): four consecutive keys at the lane's d, i.e.
+//    half of the A operand of O^T = V^T P^T for k-step u.  One DMA
+//    instruction fills blocks (2p, u, h) and (2p+1, u, h): 8 key rows x 128
+//    contiguous bytes.
+#include "attn_common.h"
+
+#include <cstdio>
+#include <cstdlib>
+#include <type_traits>
+
+namespace hkv {
+namespace {
+
+using namespace attn;
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+constexpr int kTileBytes = kBN * kD * 2;  // 16 KiB per tensor per tile
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kDmaPerTile = 2 * kTileBytes / 1024;  // wave-level 1 KiB DMA instructions
+
+// s_waitcnt for "at most n vector-memory operations outstanding" (gfx9
+// encoding; expcnt and lgkmcnt left at their maxima = not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ u32x2_t ds_read_tr(const uint8_t* p) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p)));
+}
+
+// 16-byte-per-lane buffer load written straight to LDS at `lds_addr` (the
+// wave-uniform LDS byte address; lane l lands at lds_addr + 16 l).  Issued as
+// inline assembly so that the compiler, which cannot see the LDS write, does
+// not make every later LDS read wait for all outstanding loads: ordering is
+// explicit here (s_waitcnt vmcnt before each tile's barrier).
+// M0 is written here and declared clobbered; nothing else in these kernels
+// uses M0 (tests/test_build_isa.py checks the generated code), so the
+// compiler's warning about clobbering a reserved register is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const u32x4_t rsrc, uint32_t lds_addr, int32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Raw buffer descriptor (gfx9 layout) over [base, base + bytes), uniform.
+__device__ __forceinline__ u32x4_t make_desc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4_t d;
+  d[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  d[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+  d[2] = __builtin_amdgcn_readfirstlane(bytes);
+  d[3] = 0x00020000u;
+  return d;
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)(p)));
+}
+
+template <int QDT, int KDT, int VDT, int NW, int NS>
+__global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
+    const AttnArgs a, const Scalars sc, const int32_t n_qt) {
+  static_assert(KDT != kF32 && VDT != kF32 && QDT == KDT, "16-bit inputs only");
+  static_assert(NS >= 2 && NS <= 4, "ring depth");
+  constexpr int MQK = KDT;
+  constexpr int MV = VDT;
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = NW * 32;
+  constexpr int kDmaPerWave = kDmaPerTile / NW;
+
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStageBytes];
+  __shared__ __attribute__((aligned(16))) int32_t rowtab[NS + 1][kBN];
+  __shared__ int32_t seg_start[kMaxSegments];
+  __shared__ int32_t seg_pref[kMaxSegments + 1];
+  static_assert(NS * kStageBytes >= 2 * kMaxHeads * 4, "head tables alias the ring");
+
+  const int64_t cap = a.slab_capacity;
+  const int H = a.heads;
+  const int L = a.cur_len;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
+  const int g = lane >> 5;
+
+  // The head tables of the work plan live in the (not yet used) ring.
+  int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
+  const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
+                                         a.max_segments, a.batch, n_qt, head_rows,
+                                         head_rows + kMaxHeads, seg_start, seg_pref);
+  const int32_t R = w.R;
+  const int32_t ntp = (R + kBN - 1) / kBN;
+  const int32_t ntc = (L + kBN - 1) / kBN;
+  const int32_t ntiles = ntp + ntc;
+
+  // Waves issue K or V DMA only: waves [0, 16 / kDmaPerWave) fetch K.
+  const bool k_wave = wave * kDmaPerWave < 16;
+  const int64_t cur_row0 = static_cast<int64_t>(w.bh) * L;
+  const u32x4_t d_prior = make_desc(
+      static_cast<const uint8_t*>(k_wave ? a.slab_k : a.slab_v) + static_cast<int64_t>(w.b) * cap * kD * 2,
+      static_cast<uint32_t>(cap * kD * 2));
+  const u32x4_t d_cur = make_desc(
+      static_cast<const uint8_t*>(k_wave ? a.cur_k : a.cur_v) + cur_row0 * kD * 2,
+      static_cast<uint32_t>(L * kD * 2));
+
+  // Per-lane key index and byte offset within the key row for each of this
+  // wave's DMA instructions (tile independent).
+  int dma_key[kDmaPerWave];
+  int dma_col[kDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    const int q = wave * kDmaPerWave + i;
+    if (k_wave) {  // K block (kb, ks) = (q / 8, q % 8)
+      dma_key[i] = (q >> 3) * 32 + (lane & 31);
+      dma_col[i] = (q & 7) * 32 + (lane >> 5) * 16;
+    } else {  // V blocks (2p, u, h), (2p + 1, u, h) with q - 16 = (2u + h) * 2 + p
+      const int qv = q - 16;
+      const int lp = lane & 31;
+      const int db = 2 * (qv & 1) + (lane >> 5);
+      dma_key[i] = 16 * (qv >> 2) + 8 * ((qv >> 1) & 1) + 4 * (lp >> 4) + ((lp & 7) >> 1);
+      dma_col[i] = 2 * (db * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
+    }
+  }
+  const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
+
+  auto issue_tile = [&](int tile) {
+    const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
+    if (tile < ntp) {
+      const int32_t* rt = rowtab[tile % (NS + 1)];
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int pr = rt[dma_key[i]];
+        dma16(d_prior, dst + i * 1024, pr < 0 ? -1 : pr * 256 + dma_col[i]);
+      }
+    } else {
+      const int row0 = (tile - ntp) * kBN;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int row = row0 + dma_key[i];
+        dma16(d_cur, dst + i * 1024, row < L ? row * 256 + dma_col[i] : -1);
+      }
+    }
+  };
+
+  int cur_seg = 0;
+  if (wave == 0) {
+    for (int p = 0; p < NS && p < ntp; ++p)
+      fill_rowtab(p, rowtab[p % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < ntiles) issue_tile(p);
+
+  // Q fragments (B operand of S^T = K Q^T): query row, d = 16ks + 8g .. +7
+  const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
+  u32x4_t qf[8];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * 2, static_cast<uint32_t>(L * kD * 2));
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
+      qf[ks] ^= sc.q_sign;
+    }
+  }
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
+  float m_run = -1e30f;
+  float l_run = 0.f;
+  const float thresh = sc.c > 0.f ? kRescaleLog2 / sc.c : 0.f;
+
+  for (int t = 0; t < ntiles; ++t) {
+    // This wave's DMA for tile t is complete once at most the later tiles'
+    // instructions are outstanding (the older Q loads are then complete too).
+    const int later = min(NS - 2, ntiles - 1 - t);
+    if (later <= 0) wait_vmcnt<0>();
+    else if (later == 1) wait_vmcnt<kDmaPerWave>();
+    else wait_vmcnt<2 * kDmaPerWave>();
+    __syncthreads();
+    // tile t + NS - 1 reuses the stage of tile t - 1, finished by every wave
+    if (t + NS - 1 < ntiles) issue_tile(t + NS - 1);
+    if (wave == 0 && t + NS < ntp)
+      fill_rowtab(t + NS, rowtab[(t + NS) % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref);
+
+    const uint8_t* kst = ring + (t % NS) * kStageBytes + lane * 16;
+    const uint8_t* vst = ring + (t % NS) * kStageBytes + kTileBytes + lane * 8;
+    f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kst + (kb * 8 + ks) * 1024);
+        s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
+      }
+    const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
+    softmax_tile(s, oacc, m_run, l_run, sc.c, thresh, valid, g);
+#pragma unroll
+    for (int u = 0; u < kBN / 16; ++u) {
+      const u32x4_t pf = p_operand<MV>(s, u);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int blk = (db >> 1) * 1024 + (db & 1) * 512;
+        const u32x2_t lo = ds_read_tr(vst + (u * 4 + 0) * 1024 + blk);
+        const u32x2_t hi = ds_read_tr(vst + (u * 4 + 2) * 1024 + blk);
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[db] = mfma32<MV>(vf, pf, oacc[db]);
+      }
+    }
+  }
+  // no DMA is outstanding here: the last tile waited for vmcnt(0)
+  write_output<QDT>(oacc, m_run, l_run, sc.scale_abs, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+}
+
+struct Shape {
+  int nw;
+  int ns;
+};
+
+// Waves per workgroup x ring depth.  HKV_ATTN_DIRECT (read once) selects
+// another compiled shape for tuning sweeps: "4x2" (default: two workgroups
+// per CU), "8x3", "8x4" (one workgroup per CU).
+Shape shape() {
+  static Shape s = [] {
+    Shape r{4, 2};
+    if (const char* e = std::getenv("HKV_ATTN_DIRECT")) {
+      int nw = 0, ns = 0;
+      if (std::sscanf(e, "%dx%d", &nw, &ns) == 2 &&
+          ((nw == 8 && (ns == 3 || ns == 4)) || (nw == 4 && ns == 2)))
+        r = Shape{nw, ns};
+    }
+    return r;
+  }();
+  return s;
+}
+
+template <int DT, int VDT>
+hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
+  const Shape sh = shape();
+  const int32_t bm = sh.nw * 32;
+  const int32_t n_qt = (a.cur_len + bm - 1) / bm;
+  const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  if (sh.nw == 8 && sh.ns == 4)
+    seg_attn_direct_kernel<DT, DT, VDT, 8, 4><<<grid, 512, 0, st>>>(a, s, n_qt);
+  else if (sh.nw == 8)
+    seg_attn_direct_kernel<DT, DT, VDT, 8, 3><<<grid, 512, 0, st>>>(a, s, n_qt);
+  else
+    seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<grid, 256, 0, st>>>(a, s, n_qt);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool attention_direct_supported(const AttnArgs& a) {
+  const bool k16 = a.k_dtype == kBF16 || a.k_dtype == kF16;
+  const bool v16 = a.v_dtype == kBF16 || a.v_dtype == kF16;
+  return k16 && v16 && a.q_dtype == a.k_dtype && a.heads <= attn::kMaxHeads;
+}
+
+hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream) {
+  if (!attention_direct_supported(a)) return hipErrorInvalidValue;
+  if (a.k_dtype == kBF16)
+    return a.v_dtype == kBF16 ? launch<kBF16, kBF16>(a, s, stream) : launch<kBF16, kF16>(a, s, stream);
+  return a.v_dtype == kBF16 ? launch<kF16, kBF16>(a, s, stream) : launch<kF16, kF16>(a, s, stream);
+}
+
+}  // namespace hkv

@@ -1,0 +1,57 @@
+"""Checks on the generated gfx950 code (host-side compile, no GPU needed).
+
+The direct-to-LDS attention kernel writes M0 inside its DMA inline assembly
+and declares it clobbered; that is only sound while no compiler-generated
+instruction relies on M0.  This compiles the kernel to assembly and checks
+that every M0 reference sits inside an inline-assembly block, and that no
+kernel spills registers to scratch.
+"""
+
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "heatkv_amd", "csrc")
+
+
+def _hipcc():
+    cand = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "bin", "hipcc")
+    return cand if os.path.exists(cand) else shutil.which("hipcc")
+
+
+def _asm(src, tmp_path):
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "k.s"
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", "-S",
+           "--cuda-device-only", os.path.join(CSRC, src), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True)
+    return out.read_text()
+
+
+@pytest.mark.parametrize("src", ["seg_attn_direct.hip"])
+def test_m0_only_inside_inline_asm(src, tmp_path):
+    text = _asm(src, tmp_path)
+    inside = False
+    for line in text.splitlines():
+        s = line.strip()
+        if s.startswith(";;#ASMSTART"):
+            inside = True
+        elif s.startswith(";;#ASMEND"):
+            inside = False
+        elif not inside and not s.startswith(";") and re.search(r"\bm0\b", s):
+            pytest.fail(f"compiler-generated M0 use outside the DMA asm: {s}")
+
+
+@pytest.mark.parametrize("src", ["seg_attn_direct.hip", "seg_attn_staged.hip", "pack.hip"])
+def test_no_scratch_spills(src, tmp_path):
+    text = _asm(src, tmp_path)
+    assert "scratch_store" not in text and "scratch_load" not in text
