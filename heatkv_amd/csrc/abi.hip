@@ -136,6 +136,12 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
     return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
   if (slab_capacity > 0 && (!slab_k || !slab_v))
     return fail(HKV_ERR_INVALID_ARG, "null slab pointer with nonzero capacity");
+  // The kernels address one batch row of the slab and one (batch, head) of
+  // the current tensors through 32-bit buffer offsets.
+  const int64_t row_bytes = static_cast<int64_t>(head_dim) * 4;
+  if (slab_capacity * row_bytes >= 0x7fffffffLL || static_cast<int64_t>(cur_len) * row_bytes >= 0x7fffffffLL)
+    return fail(HKV_ERR_UNSUPPORTED, "slab rows per batch row and current_len must stay below %lld",
+                static_cast<long long>(0x7fffffffLL / row_bytes));
   hkv::AttnArgs a{};
   a.q = q;
   a.slab_k = slab_k;

@@ -218,45 +218,68 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
 }
 
 // Row table of prior tile `tile` (wave 0, one entry per lane per 64 keys):
-// stream position -> slab row, or -1 past R.  `cur_seg` walks forward with the
-// tiles (callers fill tiles in increasing order).
+// stream position -> slab row * ROW_BYTES, or `past_end` past R.  With
+// ROW_BYTES = 1 the entries are row indices.  `cur_seg` walks forward with
+// the tiles (callers fill tiles in increasing order).
+template <int ROW_BYTES = 1>
 __device__ __forceinline__ void fill_rowtab(int tile, int32_t* rowtab, int& cur_seg, int nseg, int R,
-                                            const int32_t* seg_start, const int32_t* seg_pref) {
+                                            const int32_t* seg_start, const int32_t* seg_pref,
+                                            int32_t past_end = -1) {
   const int lane = threadIdx.x & 63;
   const int j0 = tile * kBN;
   while (cur_seg < nseg && seg_pref[cur_seg + 1] <= j0) ++cur_seg;
   const int j = j0 + lane;
-  int row = -1;
+  int32_t row = past_end;
   if (j < R) {
     int s = cur_seg;
     while (seg_pref[s + 1] <= j) ++s;
-    row = seg_start[s] + (j - seg_pref[s]);
+    row = (seg_start[s] + (j - seg_pref[s])) * ROW_BYTES;
   }
   rowtab[lane] = row;
 }
 
 // ---------------------------------------------------------------- softmax
 
+// Maximum / sum of v over lanes l and l ^ 32 (the two lanes that hold one
+// query's scores) without an LDS round trip: v_permlane32_swap exchanges the
+// lane halves of two registers.
+__device__ __forceinline__ float pair_max(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+               __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+
+__device__ __forceinline__ float pair_sum(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+         __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 // Online softmax of one 64-key tile held as S^T blocks (keys 32kb + 8(j>>2) +
-// 4g + (j&3), query = lane & 31).  Overwrites s with p = exp2(c (s - m)) (0 for
-// keys >= valid_keys), rescales oacc / l_run when the reference max moves.
+// 4g + (j&3), query = lane & 31).  Overwrites s with p = exp2(c (s - m)),
+// rescales oacc / l_run when the reference max moves.  Keys >= valid_keys
+// get score -inf, hence p = exp2(-inf) = 0 (the launcher guarantees c > 0),
+// so no second mask is needed after the exponentials.
 __device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[4], float& m_run,
                                              float& l_run, float c, float thresh, int valid_keys,
                                              int g) {
-  const bool partial = valid_keys < kBN;
-  if (partial) {
+  if (valid_keys < kBN) {
+    // key index 32kb + 8(j>>2) + 4g + (j&3) >= valid  <=>  constant >= valid - 4g
+    const int lim = valid_keys - 4 * g;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = -__builtin_inff();
+        if (kb * 32 + 8 * (j >> 2) + (j & 3) >= lim) s[kb][j] = -__builtin_inff();
   }
   float mx = s[0][0];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = pair_max(mx);
   if (__any(mx - m_run > thresh)) {
     const float m_new = fmaxf(m_run, mx);
     const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
@@ -270,19 +293,12 @@ __device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int j = 0; j < 16; ++j) s[kb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c, -mc));
-  if (partial) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (kb * 32 + 8 * (j >> 2) + 4 * g + (j & 3) >= valid_keys) s[kb][j] = 0.f;
-  }
-  float psum = 0.f;
+  float psum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) psum += s[kb][j];
-  l_run += psum;
+    for (int j = 0; j < 16; ++j) psum[2 * kb + (j >> 3)] += s[kb][j];
+  l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
 }
 
 // P^T B-operand for PV k-step u (keys 16u + {4g..4g+3, 8+4g..8+4g+3}).
@@ -299,13 +315,12 @@ __device__ __forceinline__ u32x4_t p_operand(const f32x16_t (&s)[2], int u) {
 }
 
 // O = acc / l to out[b, q, h*D + d] (d = 32db + 8(j>>2) + 4g + (j&3)), and
-// lse = scale * m + ln(l) for the lane's query.
+// lse = ln(2) (c m + log2(l)) for the lane's query (c = scale log2(e)).
 template <int QDT>
 __device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_run, float l_run,
-                                             float scale_abs, void* out, float* lse, int64_t b,
-                                             int64_t h, int32_t qrow, int L, int H, int64_t bh,
-                                             int g) {
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+                                             float c, void* out, float* lse, int64_t b, int64_t h,
+                                             int32_t qrow, int L, int H, int64_t bh, int g) {
+  const float l_tot = pair_sum(l_run);
   const float inv = 1.f / l_tot;
   if (qrow >= L) return;
   const int64_t out_row = (b * L + qrow) * (static_cast<int64_t>(H) * kD) + h * kD;
@@ -320,15 +335,20 @@ __device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_
       v[3] = oacc[db][4 * jb + 3] * inv;
       store4<QDT>(out, out_row + db * 32 + 8 * jb + 4 * g, v);
     }
-  if (lse != nullptr && g == 0) lse[bh * L + qrow] = m_run * scale_abs + __logf(l_tot);
+  if (lse != nullptr && g == 0) lse[bh * L + qrow] = (m_run * c + __log2f(l_tot)) * 0.6931471805599453f;
 }
 
 // Launch plumbing shared by the two kernels.
 struct Scalars {
-  float c;          // |scale| * log2(e)
-  float scale_abs;  // |scale|
+  float c;          // max(|scale| * log2(e), kMinC): the exp2 multiplier, > 0
+  float thresh;     // kRescaleLog2 / c: score growth (score units) that moves the max
   uint32_t q_sign;  // 0x80008000 when scale < 0: q's 16-bit operands are negated
 };
+
+// Smallest exp2 multiplier.  A softmax scale of 0 (uniform attention) runs
+// with c = kMinC: every p is then exp2(~0) and the result is the uniform
+// average, while -inf still masks the keys past a tile's end.
+constexpr float kMinC = 1e-30f;
 
 }  // namespace attn
 

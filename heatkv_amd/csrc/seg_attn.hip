@@ -22,8 +22,9 @@ bool force_staged() {
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.heads > attn::kMaxHeads || a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
   attn::Scalars s;
-  s.scale_abs = a.softmax_scale < 0.f ? -a.softmax_scale : a.softmax_scale;
-  s.c = s.scale_abs * attn::kLog2e;
+  const float scale_abs = a.softmax_scale < 0.f ? -a.softmax_scale : a.softmax_scale;
+  s.c = fmaxf(scale_abs * attn::kLog2e, attn::kMinC);
+  s.thresh = attn::kRescaleLog2 / s.c;
   s.q_sign = a.softmax_scale < 0.f ? 0x80008000u : 0u;
   if (!force_staged() && attention_direct_supported(a)) return launch_attention_direct(a, s, stream);
   return launch_attention_staged(a, s, stream);

@@ -117,19 +117,25 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
   const int32_t ntiles = ntp + ntc;
 
   // Waves issue K or V DMA only: waves [0, 16 / kDmaPerWave) fetch K.
+  // Byte ranges are below 2^31 (checked by the C ABI), so a row-table
+  // sentinel of 2^31 plus a column offset is past the end of the prior
+  // descriptor and reads zeros.
   const bool k_wave = wave * kDmaPerWave < 16;
   const int64_t cur_row0 = static_cast<int64_t>(w.bh) * L;
   const u32x4_t d_prior = make_desc(
       static_cast<const uint8_t*>(k_wave ? a.slab_k : a.slab_v) + static_cast<int64_t>(w.b) * cap * kD * 2,
       static_cast<uint32_t>(cap * kD * 2));
-  const u32x4_t d_cur = make_desc(
-      static_cast<const uint8_t*>(k_wave ? a.cur_k : a.cur_v) + cur_row0 * kD * 2,
-      static_cast<uint32_t>(L * kD * 2));
+  const uint8_t* const cur_base =
+      static_cast<const uint8_t*>(k_wave ? a.cur_k : a.cur_v) + cur_row0 * kD * 2;
+  const uint32_t cur_bytes = static_cast<uint32_t>(L * kD * 2);
+  constexpr int32_t kPastEnd = static_cast<int32_t>(0x80000000u);
 
   // Per-lane key index and byte offset within the key row for each of this
-  // wave's DMA instructions (tile independent).
+  // wave's DMA instructions (tile independent), and the byte offset of that
+  // element within a tile of current rows.
   int dma_key[kDmaPerWave];
   int dma_col[kDmaPerWave];
+  int dma_off[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
     const int q = wave * kDmaPerWave + i;
@@ -143,32 +149,31 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
       dma_key[i] = 16 * (qv >> 2) + 8 * ((qv >> 1) & 1) + 4 * (lp >> 4) + ((lp & 7) >> 1);
       dma_col[i] = 2 * (db * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
     }
+    dma_off[i] = dma_key[i] * (kD * 2) + dma_col[i];
   }
   const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
 
   auto issue_tile = [&](int tile) {
     const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
     if (tile < ntp) {
+      // rowtab holds slab row * 256 (or the 2^31 sentinel past R)
       const int32_t* rt = rowtab[tile % (NS + 1)];
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int pr = rt[dma_key[i]];
-        dma16(d_prior, dst + i * 1024, pr < 0 ? -1 : pr * 256 + dma_col[i]);
-      }
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
     } else {
-      const int row0 = (tile - ntp) * kBN;
+      // The descriptor starts at the tile's first row and ends at the last
+      // current row, so rows past L read zeros with no per-lane check.
+      const uint32_t skip = static_cast<uint32_t>(tile - ntp) * (kBN * kD * 2);
+      const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int row = row0 + dma_key[i];
-        dma16(d_cur, dst + i * 1024, row < L ? row * 256 + dma_col[i] : -1);
-      }
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
     }
   };
 
   int cur_seg = 0;
   if (wave == 0) {
     for (int p = 0; p < NS && p < ntp; ++p)
-      fill_rowtab(p, rowtab[p % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref);
+      fill_rowtab<kD * 2>(p, rowtab[p % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
   }
   __syncthreads();
 #pragma unroll
@@ -193,7 +198,6 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
   for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
   float m_run = -1e30f;
   float l_run = 0.f;
-  const float thresh = sc.c > 0.f ? kRescaleLog2 / sc.c : 0.f;
 
   for (int t = 0; t < ntiles; ++t) {
     // This wave's DMA for tile t is complete once at most the later tiles'
@@ -206,7 +210,8 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
     // tile t + NS - 1 reuses the stage of tile t - 1, finished by every wave
     if (t + NS - 1 < ntiles) issue_tile(t + NS - 1);
     if (wave == 0 && t + NS < ntp)
-      fill_rowtab(t + NS, rowtab[(t + NS) % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref);
+      fill_rowtab<kD * 2>(t + NS, rowtab[(t + NS) % (NS + 1)], cur_seg, w.nseg, R, seg_start,
+                          seg_pref, kPastEnd);
 
     const uint8_t* kst = ring + (t % NS) * kStageBytes + lane * 16;
     const uint8_t* vst = ring + (t % NS) * kStageBytes + kTileBytes + lane * 8;
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
         s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
       }
     const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
-    softmax_tile(s, oacc, m_run, l_run, sc.c, thresh, valid, g);
+    softmax_tile(s, oacc, m_run, l_run, sc.c, sc.thresh, valid, g);
 #pragma unroll
     for (int u = 0; u < kBN / 16; ++u) {
       const u32x4_t pf = p_operand<MV>(s, u);
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
     }
   }
   // no DMA is outstanding here: the last tile waited for vmcnt(0)
-  write_output<QDT>(oacc, m_run, l_run, sc.scale_abs, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
 }
 
 struct Shape {

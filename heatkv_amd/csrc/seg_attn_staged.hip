@@ -160,7 +160,6 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
   float m_run = -1e30f;
   float l_run = 0.f;
-  const float thresh = sc.c > 0.f ? kRescaleLog2 / sc.c : 0.f;
   const uint8_t* k_lane = k_lds + (lane & 31) * kKPitch + g * 16;
   const uint8_t* v_lane = vt_lds + (lane & 31) * kVtPitch + g * 8;
 
@@ -185,7 +184,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
         s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
       }
     const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
-    softmax_tile(s, oacc, m_run, l_run, sc.c, thresh, valid, g);
+    softmax_tile(s, oacc, m_run, l_run, sc.c, sc.thresh, valid, g);
 #pragma unroll
     for (int u = 0; u < kBN / 16; ++u) {
       const u32x4_t pf = p_operand<MV>(s, u);
@@ -200,7 +199,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
     }
     __syncthreads();
   }
-  write_output<QDT>(oacc, m_run, l_run, sc.scale_abs, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
 }
 
 template <int QDT, int KDT, int VDT>
