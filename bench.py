@@ -2,15 +2,22 @@
 
 One step = one ``fused_real_pruning_flat_segmented_attention`` call of the
 final 64x64 scale (B=2, H=16, D=128, 4096 queries, budget-0.1 slab over the
-6425-token prior; seed 1) with its inputs resident in HBM.  The slab is packed
-once before timing (the final scale appends nothing).  Prints one JSON line.
+6425-token prior, seed 1) with its inputs resident in HBM.  The slab is packed
+once before timing (the final scale appends nothing).  ``--warmup`` untimed
+steps, then ``--steps`` back-to-back steps between two HIP events recorded on
+the stream the kernel runs on; prints one JSON line.
 
-``value`` is attention TFLOP/s counted as sum_(b,h) 4 L (R_h + L) D with R_h
-the retained prior rows (no padding, no masked lanes).  ``roofline`` prices
-the attention kernel against the bf16 dense MFMA peak, from its average
-launch duration measured with HIP events on the stream it runs on.
-``cpu_baseline`` times the numpy oracle (fp32, the reference CPU path's
-gather + softmax) on the host over the whole step, on rank 0.
+* ``value``: attention TFLOP/s over the timed steps, FLOPs counted as
+  sum_(b,h) 4 L (R_h + L) D with R_h the retained prior rows (no padding, no
+  masked lanes).
+* ``roofline``: the attention kernel against the bf16 dense MFMA peak; its
+  average duration is the timed region / steps (the step is that one kernel).
+  ``traffic`` is the HBM bytes per launch from the committed rocprofv3
+  FETCH_SIZE / WRITE_SIZE summary in profiles/ (copy-calibrated).
+* ``compaction``: the slab fill (one append launch per kept prior scale)
+  against HBM bandwidth, timed separately.
+* ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
+  softmax, restated) on the host cores over whole steps, rank 0 only.
 """
 
 from __future__ import annotations
@@ -28,64 +35,57 @@ if ROOT not in sys.path:
 
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BPS = 8.0e12     # MI355X HBM3E
+PROFILES = os.path.join(ROOT, "profiles")
+ATTN_KERNEL = "seg_attn_direct_kernel"
 
 
 def parse():
-    ap = argparse.ArgumentParser(description=__doc__)
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
-    ap.add_argument("--budget", type=float, default=None)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5],
+                    help="final-step workload (2 = the 2B 1024^2 final scale)")
+    ap.add_argument("--budget", type=float, default=None, help="keep budget (configs 1, 2, 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-repeats", type=int, default=3)
+    ap.add_argument("--cpu-repeats", type=int, default=10)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE pass can scale its counters")
     return ap.parse_args()
 
 
-def time_attention(wl, device, steps, warmup):
-    import torch
-
-    from heatkv_amd import fused_real_pruning_flat_segmented_attention
+def attention_call(wl, device):
+    """Inputs of one final-step call on ``device`` (slab packed by the HIP pack kernel)."""
     from heatkv_amd import workloads as W
 
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
-    kw = dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
-              segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale)
+    return dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
+                segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale)
+
+
+def time_attention(kw, device, steps, warmup):
+    """Milliseconds per step over ``steps`` back-to-back calls (HIP events on the kernel's stream)."""
+    import torch
+
+    from heatkv_amd import fused_real_pruning_flat_segmented_attention as attn
+
     for _ in range(warmup):
-        fused_real_pruning_flat_segmented_attention(**kw)
-    torch.cuda.synchronize(device)
+        attn(**kw)
     stream = torch.cuda.current_stream(device)
-    # (1) K back-to-back steps between two events: time per step
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(device)
+    host0 = time.perf_counter()
     t0.record(stream)
     for _ in range(steps):
-        fused_real_pruning_flat_segmented_attention(**kw)
+        attn(**kw)
     t1.record(stream)
+    host_us = (time.perf_counter() - host0) / steps * 1e6
     torch.cuda.synchronize(device)
-    ms_per_step = t0.elapsed_time(t1) / steps
-    # (2) per-launch durations, one event pair around each launch
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
-    for a, b in evs:
-        a.record(stream)
-        fused_real_pruning_flat_segmented_attention(**kw)
-        b.record(stream)
-    torch.cuda.synchronize(device)
-    kern = [a.elapsed_time(b) for a, b in evs]
-    # (3) host cost of one call (enqueue only; the GPU is left to drain)
-    t_host = time.perf_counter()
-    for _ in range(steps):
-        fused_real_pruning_flat_segmented_attention(**kw)
-    host_us = (time.perf_counter() - t_host) / steps * 1e6
-    torch.cuda.synchronize(device)
-    return ms_per_step, statistics.mean(kern), statistics.median(kern), host_us
+    return t0.elapsed_time(t1) / steps, host_us
 
 
 def time_pack(wl, device, reps=20):
@@ -111,10 +111,10 @@ def time_pack(wl, device, reps=20):
         nbytes += B * plan.slots * D * esz * 2
     for c in calls:
         pack_flat_segments_kv(**c)
-    torch.cuda.synchronize(device)
     stream = torch.cuda.current_stream(device)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
     t0.record(stream)
     for _ in range(reps):
         for c in calls:
@@ -138,7 +138,7 @@ def copy_calibration(device, mib):
 
 
 def cpu_baseline(wl, repeats):
-    """Numpy oracle (fp32) over the whole step on the host cores."""
+    """Numpy oracle (fp32) over whole steps on the host cores."""
     import numpy as np
 
     from oracle import segmented_attention as oattn
@@ -151,7 +151,7 @@ def cpu_baseline(wl, repeats):
         threads = os.cpu_count() or 1
     f = lambda t: t.float().numpy()  # noqa: E731
     st, en, ct = (t.numpy() for t in wl.tables())
-    # slab as the host sees it: place each live segment's rows at its offset
+    # slab as the host sees it: each live segment's rows at its offset
     B, H, _, D = wl.prior_k.shape
     slab_k = np.zeros((B, wl.schedule.capacity, D), np.float32)
     slab_v = np.zeros_like(slab_k)
@@ -167,15 +167,29 @@ def cpu_baseline(wl, repeats):
         oattn.flat_segmented_attention(*args)
         times.append(time.perf_counter() - t)
     sec = statistics.median(times)
-    return dict(value=wl.attention_flops() / sec / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"whole step ({wl.name}: B={wl.batch}, H={wl.heads}, L={wl.cur_len}), "
-                       f"numpy fp32 oracle, median of {repeats}", ms_per_step=sec * 1e3)
+    return dict(value=round(wl.attention_flops() / sec / 1e12, 4), unit="TFLOP/s", cores=threads,
+                kind="port",
+                sample=f"{repeats} whole steps of {wl.name} (B={wl.batch}, H={wl.heads}, "
+                       f"L={wl.cur_len}), numpy fp32 oracle, median",
+                ms_per_step=round(sec * 1e3, 2))
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per dispatch of ``kernel`` on ``workload`` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    path = os.path.join(PROFILES, f"{kernel}__{workload}.traffic.json")
+    try:
+        with open(path) as fh:
+            rec = json.load(fh)
+        return int(rec["bytes_per_dispatch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this path needs no collective); got --gpus {args.gpus}",
+        print(f"bench.py measures one GPU only (this path has no collective); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -185,14 +199,15 @@ def main():
     device = torch.device("cuda:0")
     wl = W.config(args.config, budget=args.budget)
     flops = wl.attention_flops()
-    ms_step, kern_mean, kern_med, host_us = time_attention(wl, device, args.steps, args.warmup)
-    achieved = flops / (kern_mean * 1e-3)
+    kw = attention_call(wl, device)
+    ms_step, host_us = time_attention(kw, device, args.steps, args.warmup)
+    achieved = flops / (ms_step * 1e-3)
     pack_ms, pack_bytes, pack_calls = time_pack(wl, device)
     if args.copy_calib_mib > 0:
         copy_calibration(device, args.copy_calib_mib)
     rec = {
         "metric": "segmented-attn TFLOP/s & % bf16 MFMA peak; ms per scale step (2B, 1024^2)",
-        "value": round(flops / (ms_step * 1e-3) / 1e12, 3),
+        "value": round(achieved / 1e12, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -212,9 +227,9 @@ def main():
         "pct_of_bf16_peak": round(100.0 * achieved / PEAK_BF16_FLOPS, 2),
         "roofline": {
             "bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": PEAK_BF16_FLOPS / 1e12,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_FLOPS, 4), "traffic": None,
-            "kernel": "seg_attn_direct_kernel", "kernel_ms_mean": round(kern_mean, 5),
-            "kernel_ms_median": round(kern_med, 5),
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_FLOPS, 4),
+            "traffic": measured_traffic(ATTN_KERNEL, wl.name),
+            "kernel": ATTN_KERNEL, "kernel_ms_mean": round(ms_step, 5),
         },
         "host_us_per_call": round(host_us, 1),
         "compaction": {

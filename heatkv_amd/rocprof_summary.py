@@ -1,0 +1,145 @@
+"""Summaries of rocprofv3 CSV output for the kernels of this package.
+
+Three reports, each written as a short text/JSON file under ``profiles/``:
+
+* ``stats``   -- the ``*_kernel_stats.csv`` of a ``--kernel-trace --stats`` run
+  as a markdown table (calls, average / min / max duration per kernel).
+* ``traffic`` -- HBM bytes per dispatch of one kernel from two ``--pmc`` runs
+  (``FETCH_SIZE``, then ``WRITE_SIZE``; both in KiB per dispatch).  Each
+  counter is scaled by what it reads for a plain device copy of known size
+  in the same run (``bench.py --copy-calib-mib N`` launches it): the copy
+  moves N MiB each way, so ``factor = N MiB / counter(copy)``.
+* ``counters`` -- mean per-dispatch values of any other ``--pmc`` counters.
+
+Usage::
+
+    python -m heatkv_amd.rocprof_summary stats KT_DIR --out profiles/x.md --cmd "..."
+    python -m heatkv_amd.rocprof_summary traffic --fetch F.csv --write W.csv \\
+        --kernel seg_attn_direct --calib-mib 512 --out profiles/x.json --cmd "..."
+    python -m heatkv_amd.rocprof_summary counters C.csv [C2.csv ...] --kernel seg_attn_direct \\
+        --out profiles/x.md --cmd "..."
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import statistics
+from collections import defaultdict
+from typing import Dict, List
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def _rows(path: str) -> List[dict]:
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def per_dispatch(path: str, kernel_substr: str) -> Dict[str, List[float]]:
+    """``{counter: [value per dispatch]}`` of the dispatches whose name contains ``kernel_substr``."""
+    out: Dict[str, List[float]] = defaultdict(list)
+    for r in _rows(path):
+        if kernel_substr in r["Kernel_Name"]:
+            out[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return dict(out)
+
+
+def stats_markdown(kt_dir: str, cmd: str) -> str:
+    paths = glob.glob(os.path.join(kt_dir, "*kernel_stats.csv"))
+    if not paths:
+        raise FileNotFoundError(f"no *kernel_stats.csv under {kt_dir}")
+    lines = [
+        "# rocprofv3 kernel-trace statistics",
+        "",
+        f"Command: `{cmd}`",
+        "",
+        "| kernel | calls | avg us | min us | max us | share % |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for r in _rows(paths[0]):
+        name = r["Name"]
+        if len(name) > 110:
+            name = name[:107] + "..."
+        lines.append(
+            f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+            f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |"
+        )
+    return "\n".join(lines) + "\n"
+
+
+def traffic(fetch_csv: str, write_csv: str, kernel_substr: str, calib_mib: int, cmd: str) -> dict:
+    """Calibrated HBM read / write bytes per dispatch of ``kernel_substr``."""
+    calib_kib = calib_mib * 1024.0
+    res = {"kernel": kernel_substr, "calibration_copy_mib": calib_mib, "command": cmd}
+    for label, path, counter in (("read", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        kern = per_dispatch(path, kernel_substr).get(counter, [])
+        copy = per_dispatch(path, COPY_KERNEL).get(counter, [])
+        if not kern or not copy:
+            raise ValueError(f"{path}: no {counter} values for {kernel_substr!r} or the copy kernel")
+        copy_kib = max(copy)  # the calibration copies are the largest copyBuffer dispatches
+        factor = calib_kib / copy_kib
+        mean_kib = statistics.mean(kern)
+        res[f"{counter}_kib_per_dispatch"] = round(mean_kib, 3)
+        res[f"{counter}_copy_kib"] = round(copy_kib, 3)
+        res[f"{label}_factor"] = round(factor, 4)
+        res[f"{label}_bytes"] = int(round(mean_kib * factor * 1024.0))
+        res[f"{label}_dispatches"] = len(kern)
+    res["bytes_per_dispatch"] = res["read_bytes"] + res["write_bytes"]
+    return res
+
+
+def counters_markdown(paths: List[str], kernel_substr: str, cmd: str) -> str:
+    vals: Dict[str, List[float]] = {}
+    for p in paths:
+        vals.update(per_dispatch(p, kernel_substr))
+    lines = [
+        f"# rocprofv3 counters: `{kernel_substr}` (mean per dispatch)",
+        "",
+        f"Command: `{cmd}`",
+        "",
+        "| counter | value | dispatches |",
+        "|---|---:|---:|",
+    ]
+    for k in sorted(vals):
+        lines.append(f"| {k} | {statistics.mean(vals[k]):.0f} | {len(vals[k])} |")
+    return "\n".join(lines) + "\n"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest="what", required=True)
+    a = sub.add_parser("stats")
+    a.add_argument("kt_dir")
+    a.add_argument("--out", required=True)
+    a.add_argument("--cmd", required=True)
+    b = sub.add_parser("traffic")
+    b.add_argument("--fetch", required=True)
+    b.add_argument("--write", required=True)
+    b.add_argument("--kernel", required=True)
+    b.add_argument("--calib-mib", type=int, required=True)
+    b.add_argument("--out", required=True)
+    b.add_argument("--cmd", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("csv", nargs="+")
+    c.add_argument("--kernel", required=True)
+    c.add_argument("--out", required=True)
+    c.add_argument("--cmd", required=True)
+    args = ap.parse_args(argv)
+    if args.what == "stats":
+        text = stats_markdown(args.kt_dir, args.cmd)
+    elif args.what == "traffic":
+        text = json.dumps(traffic(args.fetch, args.write, args.kernel, args.calib_mib, args.cmd), indent=1) + "\n"
+    else:
+        text = counters_markdown(args.csv, args.kernel, args.cmd)
+    os.makedirs(os.path.dirname(os.path.abspath(args.out)), exist_ok=True)
+    with open(args.out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
+if __name__ == "__main__":
+    main()
