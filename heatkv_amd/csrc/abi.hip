@@ -119,6 +119,8 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented requires current_len > 0");
   if (batch <= 0 || heads <= 0)
     return fail(HKV_ERR_INVALID_ARG, "batch and heads must be positive (got %d, %d)", batch, heads);
+  if (heads > 1024)
+    return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented supports at most 1024 heads (got %d)", heads);
   if (elem_bytes(q_dtype) == 0 || elem_bytes(k_dtype) == 0 || elem_bytes(v_dtype) == 0)
     return fail(HKV_ERR_UNSUPPORTED,
                 "real_scale_fused_segmented supports only float16, bfloat16, or float32 tensors");
