@@ -16,6 +16,11 @@ the stream the kernel runs on; prints one JSON line.
   FETCH_SIZE / WRITE_SIZE summary in profiles/ (copy-calibrated).
 * ``compaction``: the slab fill (one append launch per kept prior scale)
   against HBM bandwidth, timed separately.
+* ``sweep``: the 2B generation sweep (32 layers x 13 scale steps, B=2,
+  H=16, per-layer static keep policies at budget 0.1): every layer-step runs
+  SegmentedLayerCache.step (dense-prefix attention, activation pack,
+  segmented attention, append), timed per image, plus a phase split from a
+  separately profiled image (the profiler synchronizes each phase).
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -49,6 +54,8 @@ def parse():
     ap.add_argument("--budget", type=float, default=None, help="keep budget (configs 1, 2, 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-repeats", type=int, default=10)
+    ap.add_argument("--no-sweep", action="store_true", help="skip the 32-layer generation sweep")
+    ap.add_argument("--sweep-images", type=int, default=3)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE pass can scale its counters")
@@ -123,6 +130,63 @@ def time_pack(wl, device, reps=20):
     torch.cuda.synchronize(device)
     ms = t0.elapsed_time(t1) / reps
     return ms, nbytes, len(calls)
+
+
+def time_sweep(device, images, layers=32, heads=16, batch=2):
+    """ms per image of the 2B generation sweep and its algorithmic attention FLOPs."""
+    import math
+
+    import torch
+
+    from heatkv_amd import phase_profile as prof
+    from heatkv_amd import workloads as W
+    from heatkv_amd.segmented_cache import SegmentedLayerCache
+
+    sides = W.SIDES_1M
+    keeps = W.sweep_keep_policies(layers=layers, heads=heads, sides=sides)
+    caches = [SegmentedLayerCache(W.schedule_from_keep(k, sides), W.removed_from_keep(k, len(sides)),
+                                  num_heads=heads) for k in keeps]
+    inputs = [W.generation_inputs(batch=batch, heads=heads, sides=sides, seed=2000 + l, device=device)
+              for l in range(layers)]
+    scale = 1.0 / math.sqrt(128)
+    flops = 0
+    for keep in keeps:
+        for t, side in enumerate(sides):
+            n = side * side
+            for h in range(heads):
+                r = sum(sides[s] ** 2 for s in W.retained_scales(keep, t, h))
+                flops += batch * 4 * n * (r + n) * 128
+
+    def image():
+        for t in range(len(sides)):
+            for l in range(layers):
+                q, k, v = inputs[l][t]
+                caches[l].step(q, k, v, t, scale)
+
+    image()
+    stream = torch.cuda.current_stream(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    t0.record(stream)
+    for _ in range(images):
+        image()
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    ms = t0.elapsed_time(t1) / images
+    prof.set_real_pruning_fast_phase_profile_enabled(True)
+    try:
+        image()
+        snap = prof.snapshot_real_pruning_fast_phase_profile()
+    finally:
+        prof.set_real_pruning_fast_phase_profile_enabled(False)
+    return dict(what=f"{layers} layers x {len(sides)} scale steps, B={batch}, H={heads}, budget 0.1, "
+                     "static per-layer keep policies (seed 1000 + layer)",
+                ms_per_image=round(ms, 3), attention_flops=flops,
+                tflops=round(flops / (ms * 1e-3) / 1e12, 1),
+                phase_gpu_ms_profiled={k: round(v, 3) for k, v in snap["cuda_ms"].items()},
+                phase_calls=snap["calls"],
+                copy_bytes_per_image=int(snap["segmented_flat_stats"].get("static_copy_bytes", 0)))
 
 
 def copy_calibration(device, mib):
@@ -239,6 +303,8 @@ def main():
             "frac_hbm": round(pack_bytes / (pack_ms * 1e-3) / PEAK_HBM_BPS, 4),
         },
     }
+    if not args.no_sweep:
+        rec["sweep"] = time_sweep(device, args.sweep_images)
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(wl, args.cpu_repeats)
     print(json.dumps(rec), flush=True)

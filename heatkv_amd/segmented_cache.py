@@ -1,0 +1,264 @@
+"""Per-layer KV state of the fused segmented path: dense prefix, slab, appends.
+
+``SegmentedLayerCache.step`` is the key/value half of the reference's patched
+``SelfAttention.forward`` (``_real_pruning_scale_specific_fast_forward``,
+enable_real_pruning_fast.py:1951-2254) for one layer and one scale: it takes
+the scale's q, k, v ``[B, H, n, D]`` (after the QKV projection, normalization
+and RoPE of the caller) and returns the attention output ``[B, n, H*D]``.
+Control flow, all device work on torch's current stream, no host sync:
+
+* dense prefix (:1972-2038): while no head of this layer is pruned at the
+  current target, attention runs over the whole dense cache ``[B, H, T, D]``
+  plus the current scale, and the cache grows by ``torch.cat``; when the next
+  target prunes a head, the dense cache is packed into the slab with the
+  schedule's activation copy items (:1639-1711 -> :888-908);
+* segmented (:2122-2155): attention over the slab segments of the target's
+  offset tables plus the current scale;
+* compact (:2176-2253): at the final scale the state is reset; otherwise the
+  current scale's kept heads are appended to the slab (:1791-1807 -> :969-995)
+  or, if the slab is not active yet, the dense cache and the current scale
+  are packed into it (:1713-1789).
+
+Every attention call is the HIP segmented-attention kernel: the dense prefix
+uses it too, with the dense cache viewed as a slab ``[B, H*T, D]`` holding one
+segment per head (the same softmax over the same keys as the reference's
+SDPA).  Every copy into the slab is the HIP pack kernel.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Callable, Dict, Mapping, Optional, Set, Tuple
+
+import torch
+
+from . import phase_profile as prof
+from .real_pruning_fused_attention import (
+    fused_real_pruning_flat_segmented_attention,
+    pack_flat_segments_kv,
+)
+from .slab_schedule import CopyPlan, SlabSchedule
+
+RemovedLookup = Callable[[int], Mapping[int, Set[int]]]
+
+
+def _env_flag(name: str, default: bool) -> bool:
+    raw = os.environ.get(name)
+    if raw is None:
+        return default
+    return raw.strip().lower() not in {"0", "false", "no", "off"}
+
+
+def baseline_prefix_enabled() -> bool:
+    """REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX (default on; enable_real_pruning_fast.py:1062-1066)."""
+    return _env_flag("REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX", True)
+
+
+def fused_softmax_mode() -> str:
+    """REAL_PRUNING_FUSED_SOFTMAX_MODE, 'exp' or 'exp2' (enable_real_pruning_fast.py:166-170)."""
+    mode = os.environ.get("REAL_PRUNING_FUSED_SOFTMAX_MODE", "exp")
+    return mode if mode in {"exp", "exp2"} else "exp"
+
+
+def has_removed(removed: Mapping[int, Set[int]]) -> bool:
+    return any(len(v) > 0 for v in removed.values())
+
+
+class SegmentedLayerCache:
+    """KV cache of one attention layer under a static slab schedule."""
+
+    def __init__(self, schedule: SlabSchedule, removed: RemovedLookup, *, num_heads: int,
+                 num_scales: Optional[int] = None):
+        self.schedule = schedule
+        self.removed = removed
+        self.num_heads = int(num_heads)
+        self.num_scales = int(schedule.num_scales if num_scales is None else num_scales)
+        self._tables_by_len: Dict[tuple, Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+        self._dense_current_plans: Dict[tuple, Tuple[CopyPlan, CopyPlan]] = {}
+        self.reset()
+
+    # ------------------------------------------------------------------ state
+
+    def reset(self) -> None:
+        """Empty cache (kv_caching(True) and the final scale; :2257-2266, :2176-2185)."""
+        self.cached_k: Optional[torch.Tensor] = None
+        self.cached_v: Optional[torch.Tensor] = None
+        self.logical_len = 0
+        self.active = False  # cached_k/v hold the slab
+
+    def _ensure_slab(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> None:
+        """Slab K/V ``[B, capacity, D]`` (:1092-1144); contents of unowned rows are undefined."""
+        cap = int(self.schedule.capacity)
+        self.cached_k = torch.empty((batch, cap, head_dim), device=device, dtype=k_dtype)
+        self.cached_v = torch.empty((batch, cap, head_dim), device=device, dtype=v_dtype)
+        prof.stat_add("storage_allocations")
+        prof.stat_add("storage_capacity_slots", cap)
+
+    # ------------------------------------------------------------------ copies
+
+    def _copy(self, plan: CopyPlan, src_k: torch.Tensor, src_v: torch.Tensor, tag) -> None:
+        """Pack ``plan``'s items from ``src`` ``[B, H, n, D]`` into the slab."""
+        if len(plan) == 0:
+            return
+        B, H, n, D = src_k.shape
+        if n != plan.sequence_len:
+            raise RuntimeError("static precomputed copy run sequence length mismatch")
+        dst_starts, src_starts, lengths = self.schedule.device_plan(plan, src_k.device, tag)
+        prof.stat_add("static_copy_calls")
+        prof.record_kv_copy("static_copy", slots=plan.slots, k_tensor=src_k, v_tensor=src_v)
+        pack_flat_segments_kv(dst_k=self.cached_k, dst_v=self.cached_v,
+                              src_k=src_k.reshape(B, H * n, D), src_v=src_v.reshape(B, H * n, D),
+                              dst_starts=dst_starts, src_starts=src_starts, lengths=lengths,
+                              max_length=plan.max_length)
+
+    def _activate_from_dense(self, dense_k, dense_v, target: int) -> None:
+        """Pack the dense cache into a new slab for ``target`` (:1639-1711)."""
+        B, H, T, D = dense_k.shape
+        self._ensure_slab(B, D, dense_k.device, dense_k.dtype, dense_v.dtype)
+        self.active = True
+        plan = self.schedule.activation_plans.get(int(target))
+        if plan is None or plan.sequence_len != T:
+            raise RuntimeError("segmented static pack: no activation plan for this cache length")
+        prof.stat_add("static_pack_state_calls")
+        self._copy(plan, dense_k, dense_v, ("activation", int(target)))
+
+    def _dense_and_current_plans(self, target: int, scale: int, old_len: int, cur_len: int):
+        """Copy items of the live segments at ``target``: sources before ``scale`` from the
+        dense cache, source ``scale`` from the current tensors (:871-967)."""
+        key = (target, scale, old_len, cur_len)
+        hit = self._dense_current_plans.get(key)
+        if hit is not None:
+            return hit
+        old, cur = [], []
+        for seg in self.schedule.live_segments(target):
+            if seg.source_scale == scale:
+                a = max(seg.scale_start, old_len) - old_len
+                b = min(seg.scale_end, old_len + cur_len) - old_len
+                if a < b:
+                    cur.append((seg.offset, seg.head * cur_len + a, b - a))
+            else:
+                b = min(seg.scale_end, old_len)
+                if seg.scale_start < b:
+                    old.append((seg.offset, seg.head * old_len + seg.scale_start, b - seg.scale_start))
+
+        def plan(items, n):
+            items.sort()
+            return CopyPlan([i[0] for i in items], [i[1] for i in items], [i[2] for i in items], n)
+
+        hit = (plan(old, old_len), plan(cur, cur_len))
+        self._dense_current_plans[key] = hit
+        return hit
+
+    # ------------------------------------------------------------------ attention
+
+    def _dense_tables(self, heads: int, T: int, device):
+        """Offset tables that present a dense cache ``[B, H, T, D]`` as a slab ``[B, H*T, D]``."""
+        key = (heads, T, str(device))
+        hit = self._tables_by_len.get(key)
+        if hit is None:
+            starts = (torch.arange(heads, dtype=torch.int32) * T).reshape(heads, 1)
+            hit = (starts.to(device), (starts + T).to(device),
+                   torch.ones((heads,), dtype=torch.int32).to(device))
+            self._tables_by_len[key] = hit
+        return hit
+
+    def _attend_dense(self, q, k, v, scale, mode):
+        B, H, L, D = q.shape
+        if self.cached_k is None or self.logical_len == 0:
+            empty = torch.zeros((H, 0), dtype=torch.int32, device=q.device)
+            tables = (empty, empty, torch.zeros((H,), dtype=torch.int32, device=q.device))
+            slab_k = slab_v = None
+        else:
+            T = self.cached_k.shape[2]
+            tables = self._dense_tables(H, T, q.device)
+            slab_k = self.cached_k.reshape(B, H * T, D)
+            slab_v = self.cached_v.reshape(B, H * T, D)
+        return fused_real_pruning_flat_segmented_attention(
+            q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=tables[0],
+            segment_ends=tables[1], segment_counts=tables[2], current_k=k, current_v=v,
+            softmax_scale=scale, softmax_mode=mode)
+
+    # ------------------------------------------------------------------ step
+
+    def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale_ind: int,
+             softmax_scale: float, softmax_mode: Optional[str] = None) -> torch.Tensor:
+        """Attention of scale ``scale_ind`` and the cache update for the next scale."""
+        mode = fused_softmax_mode() if softmax_mode is None else softmax_mode
+        final = scale_ind + 1 >= self.num_scales
+        old_len = self.logical_len
+        logical = old_len + int(k.shape[2])
+
+        if baseline_prefix_enabled() and not self.active and not has_removed(self.removed(scale_ind)):
+            # dense prefix (:1972-2038)
+            with prof.phase("attention"):
+                out = self._attend_dense(q, k, v, softmax_scale, mode)
+            if final:
+                self.reset()
+                return out
+            with prof.phase("materialize"):
+                if self.cached_k is None or old_len == 0:
+                    dense_k, dense_v = k.contiguous(), v.contiguous()
+                else:
+                    dense_k = torch.cat((self.cached_k, k), dim=2)
+                    dense_v = torch.cat((self.cached_v, v), dim=2)
+                    prof.stat_add("dense_attention_cat_calls")
+            self.logical_len = logical
+            if has_removed(self.removed(scale_ind + 1)):
+                with prof.phase("compact"):
+                    self._activate_from_dense(dense_k, dense_v, scale_ind + 1)
+            else:
+                self.cached_k, self.cached_v = dense_k, dense_v
+            return out
+
+        dense_candidate = None
+        if old_len == 0:
+            with prof.phase("attention"):
+                out = self._attend_dense(q, k, v, softmax_scale, mode)
+        elif not self.active and not has_removed(self.removed(scale_ind)):
+            with prof.phase("attention"):
+                out = self._attend_dense(q, k, v, softmax_scale, mode)
+            with prof.phase("materialize"):
+                dense_candidate = (torch.cat((self.cached_k, k), dim=2), torch.cat((self.cached_v, v), dim=2))
+                prof.stat_add("dense_attention_cat_calls")
+        else:
+            with prof.phase("materialize"):
+                if not self.active:
+                    self._activate_from_dense(self.cached_k, self.cached_v, scale_ind)
+                starts, ends, counts = self.schedule.device_tables(scale_ind, q.device)
+            with prof.phase("attention"):
+                out = fused_real_pruning_flat_segmented_attention(
+                    q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
+                    segment_starts=starts, segment_ends=ends, segment_counts=counts,
+                    current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode)
+
+        with prof.phase("compact"):
+            if final:
+                self.reset()
+                return out
+            nxt = self.removed(scale_ind + 1)
+            if not self.active and not has_removed(nxt):
+                if dense_candidate is not None:
+                    self.cached_k, self.cached_v = dense_candidate
+                elif self.cached_k is None or old_len == 0:
+                    self.cached_k, self.cached_v = k.contiguous(), v.contiguous()
+                else:
+                    self.cached_k = torch.cat((self.cached_k, k), dim=2)
+                    self.cached_v = torch.cat((self.cached_v, v), dim=2)
+            elif self.active:
+                # append the current scale's kept heads (:969-995)
+                prof.stat_add("static_append_current_calls")
+                plan = self.schedule.append_plans.get((int(scale_ind), int(scale_ind) + 1))
+                if plan is not None:
+                    self._copy(plan, k, v, ("append", int(scale_ind)))
+            else:
+                # pack the dense cache and the current scale into a new slab (:1713-1789)
+                dense_k, dense_v = self.cached_k, self.cached_v
+                self._ensure_slab(k.shape[0], k.shape[3], k.device, k.dtype, v.dtype)
+                self.active = True
+                old_plan, cur_plan = self._dense_and_current_plans(
+                    scale_ind + 1, scale_ind, old_len, int(k.shape[2]))
+                if dense_k is not None and old_len > 0:
+                    self._copy(old_plan, dense_k, dense_v, ("dense_old", scale_ind + 1, old_len))
+                self._copy(cur_plan, k, v, ("dense_cur", scale_ind + 1, int(k.shape[2])))
+        self.logical_len = logical
+        return out

@@ -217,3 +217,26 @@ def build_slab(wl: FinalStepWorkload, device, *, fill: float = float("nan")):
                               dst_starts=dst_starts, src_starts=src_starts, lengths=lengths,
                               max_length=plan.max_length)
     return slab_k, slab_v
+
+
+def generation_inputs(*, batch: int, heads: int, sides=SIDES_1M, seed: int = 0, dtype=torch.bfloat16,
+                      device="cpu", head_dim: int = HEAD_DIM):
+    """Per-scale ``(q, k, v)`` ``[B, H, n_s, D]`` of one layer over a whole generation.
+
+    N(0, 1) in fp32 from a seeded generator on ``device``, rounded to ``dtype``.
+    """
+    gen = torch.Generator(device=device).manual_seed(int(seed))
+    out = []
+    for side in sides:
+        n = int(side) * int(side)
+        shape = (batch, heads, n, head_dim)
+        q, k, v = (torch.randn(shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
+                   for _ in range(3))
+        out.append((q, k, v))
+    return out
+
+
+def retained_scales(keep: torch.Tensor, target: int, head: int) -> List[int]:
+    """Prior scales whose tokens head ``head`` attends to at ``target`` under a static keep mask."""
+    n_prior = keep.shape[1]
+    return [s for s in range(min(target, n_prior)) if bool(keep[head, s])]

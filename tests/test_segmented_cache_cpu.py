@@ -1,0 +1,108 @@
+"""Host control flow of SegmentedLayerCache on the CPU (no GPU, no HIP).
+
+The two HIP operators are replaced, for this test only, by CPU restatements
+from oracle/ (attention: oracle/segmented_attention.py; pack: oracle/pack.py)
+so the dense prefix -> activation -> segmented -> append -> reset flow of
+enable_real_pruning_fast.py:1951-2254 can be checked here: every step's
+output must equal attention over the keys a static keep policy retains, the
+phase profiler must see the reference's phases, and the slab must hold the
+retained rows bit-exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from heatkv_amd import phase_profile as prof
+from heatkv_amd import segmented_cache as sc
+from heatkv_amd import workloads as W
+from oracle import pack as opack
+from oracle import segmented_attention as oattn
+
+
+def _cpu_attention(*, q, persisted_k, persisted_v, segment_starts, segment_ends, segment_counts,
+                   current_k, current_v, softmax_scale, softmax_mode="exp", **_):
+    f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
+    out, _ = oattn.flat_segmented_attention(
+        f(q), f(persisted_k), f(persisted_v), segment_starts.numpy(), segment_ends.numpy(),
+        segment_counts.numpy(), f(current_k), f(current_v), softmax_scale)
+    return torch.from_numpy(out).to(q.dtype)
+
+
+def _cpu_pack(*, dst_k, dst_v, src_k, src_v, dst_starts, src_starts, lengths, max_length=None, **_):
+    for dst, src in ((dst_k, src_k), (dst_v, src_v)):
+        d = dst.view(torch.int16).numpy() if dst.element_size() == 2 else dst.numpy()
+        s = src.view(torch.int16).numpy() if src.element_size() == 2 else src.numpy()
+        opack.pack_flat_segments(d, s, dst_starts.tolist(), src_starts.tolist(), lengths.tolist())
+    return dst_k, dst_v
+
+
+@pytest.fixture
+def cpu_ops(monkeypatch):
+    monkeypatch.setattr(sc, "fused_real_pruning_flat_segmented_attention", _cpu_attention)
+    monkeypatch.setattr(sc, "pack_flat_segments_kv", _cpu_pack)
+
+
+def _expected(inputs, keep, t, scale):
+    """Attention of scale t over the retained prior scales + itself, per (b, h)."""
+    q, k, v = inputs[t]
+    B, H, L, D = q.shape
+    out = np.zeros((B, L, H * D), np.float32)
+    for h in range(H):
+        ks = [inputs[s][1][:, h] for s in W.retained_scales(keep, t, h)] + [k[:, h]]
+        vs = [inputs[s][2][:, h] for s in W.retained_scales(keep, t, h)] + [v[:, h]]
+        kk = torch.cat(ks, dim=1).float().numpy()
+        vv = torch.cat(vs, dim=1).float().numpy()
+        for b in range(B):
+            o, _ = oattn.flat_segmented_attention(
+                q[b:b + 1, h:h + 1].float().numpy(), None, None, np.zeros((1, 0), np.int32),
+                np.zeros((1, 0), np.int32), np.zeros(1, np.int32), kk[b][None, None], vv[b][None, None], scale)
+            out[b, :, h * D:(h + 1) * D] = o[0]
+    return out
+
+
+@pytest.mark.parametrize("baseline_prefix", ["1", "0"])
+def test_generation_flow_matches_retained_key_attention(cpu_ops, monkeypatch, baseline_prefix):
+    monkeypatch.setenv("REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX", baseline_prefix)
+    sides = (1, 2, 4, 6, 8)
+    H, B, D = 4, 2, 16
+    g = torch.Generator().manual_seed(3)
+    keep = torch.rand((H, len(sides) - 1), generator=g) < 0.5
+    keep[:, :2] = True
+    sched = W.schedule_from_keep(keep, sides)
+    cache = sc.SegmentedLayerCache(sched, W.removed_from_keep(keep, len(sides)), num_heads=H)
+    inputs = W.generation_inputs(batch=B, heads=H, sides=sides, seed=5, dtype=torch.float32, head_dim=D)
+    scale = D ** -0.5
+    prof.set_real_pruning_fast_phase_profile_enabled(True)
+    try:
+        for t, (q, k, v) in enumerate(inputs):
+            out = cache.step(q, k, v, t, scale)
+            np.testing.assert_allclose(out.numpy(), _expected(inputs, keep, t, scale), rtol=2e-5, atol=2e-5)
+            if cache.active and t + 1 < len(sides):
+                # the slab holds every segment live at t + 1, bit-exact
+                for seg in sched.live_segments(t + 1):
+                    src_k = inputs[seg.source_scale][1][:, seg.head]
+                    got = cache.cached_k[:, seg.offset:seg.offset + seg.length]
+                    assert torch.equal(got, src_k), (t, seg)
+        snap = prof.snapshot_real_pruning_fast_phase_profile()
+    finally:
+        prof.set_real_pruning_fast_phase_profile_enabled(False)
+    assert cache.logical_len == 0 and cache.cached_k is None  # reset at the final scale
+    assert snap["calls"]["attention"] == len(sides)
+    assert snap["calls"].get("compact", 0) >= 1
+    assert snap["segmented_flat_stats"]["storage_allocations"] == 1
+
+
+def test_unpruned_policy_stays_dense(cpu_ops):
+    sides = (1, 2, 4)
+    H = 2
+    keep = torch.ones((H, len(sides) - 1), dtype=torch.bool)
+    sched = W.schedule_from_keep(keep, sides)
+    cache = sc.SegmentedLayerCache(sched, W.removed_from_keep(keep, len(sides)), num_heads=H)
+    inputs = W.generation_inputs(batch=1, heads=H, sides=sides, seed=1, dtype=torch.float32, head_dim=8)
+    for t, (q, k, v) in enumerate(inputs[:-1]):
+        cache.step(q, k, v, t, 0.3)
+        assert not cache.active
+        assert cache.cached_k.shape[2] == sum(s * s for s in sides[:t + 1])
