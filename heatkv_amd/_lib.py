@@ -46,8 +46,10 @@ SIGNATURES = {
     "hkv_segmented_attention": (
         _c_i32,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
-         _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_p],
+         _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_p, _c_i64,
+         _c_p],
     ),
+    "hkv_segmented_attention_workspace_bytes": (_c_i64, [_c_i32]),
 }
 
 
@@ -108,3 +110,29 @@ def stream_handle(device: torch.device) -> int:
 
 def dtype_code(dtype: torch.dtype) -> int:
     return DTYPE_CODES.get(dtype, 0)
+
+
+# Attention workspaces, one per (device, stream): calls on one stream run in
+# order, so they can share one; calls on different streams may overlap.
+_workspaces: dict = {}
+
+
+def attention_workspace(device: torch.device):
+    """Zero-initialised workspace tensor of ``hkv_segmented_attention`` for the
+    current stream of ``device`` when HKV_ATTN_SPLIT=1 (cut the items
+    dispatched last), else None (every item whole, the default: on the
+    measured workloads the cut items' extra start-up and merge latency cancels
+    the gain in balance).  The kernels leave it zeroed, so it is allocated and
+    cleared once."""
+    if os.environ.get("HKV_ATTN_SPLIT", "0") != "1":
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None:
+        need = int(load().hkv_segmented_attention_workspace_bytes(idx))
+        if need < 0:
+            check(need)
+        ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _workspaces[key] = ws
+    return ws

@@ -111,7 +111,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
                                 int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
                                 int32_t v_dtype, float softmax_scale, int32_t use_exp2,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (head_dim != 128)
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented v1 only supports head_dim=128");
@@ -138,6 +138,18 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
     return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
   if (slab_capacity > 0 && (!slab_k || !slab_v))
     return fail(HKV_ERR_INVALID_ARG, "null slab pointer with nonzero capacity");
+  if (workspace != nullptr) {
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+      return fail(HKV_ERR_INVALID_ARG, "workspace must be 256-byte aligned");
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess)
+      return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
+    const int64_t need = hkv::tail_workspace_bytes(hkv::tail_slots(device));
+    if (need <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
+    if (workspace_bytes < need)
+      return fail(HKV_ERR_INVALID_ARG, "workspace of %lld bytes is smaller than the %lld required",
+                  static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  }
   // The kernels address one batch row of the slab and one (batch, head) of
   // the current tensors through 32-bit buffer offsets.
   const int64_t row_bytes = static_cast<int64_t>(head_dim) * 4;
@@ -164,10 +176,19 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   a.q_dtype = q_dtype;
   a.k_dtype = k_dtype;
   a.v_dtype = v_dtype;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace != nullptr ? workspace_bytes : 0;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int64_t hkv_segmented_attention_workspace_bytes(int32_t device) {
+  const int64_t need = hkv::tail_workspace_bytes(hkv::tail_slots(device));
+  if (need <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
+  ok();
+  return need;
 }
 
 }  // extern "C"

@@ -21,7 +21,9 @@
 //  * exp2 with scale * log2(e) folded into one FMA per score; the running max
 //    is moved lazily (only when a row grows by more than 2^8).
 //  * Work items are ordered heaviest head first (longest-processing-time
-//    order); the dispatcher fills free CU slots in workgroup-id order.
+//    order); the dispatcher fills free CU slots in workgroup-id order.  The
+//    16-bit kernel can also cut the items dispatched last into parts of
+//    their key-tile stream (tail split, below).
 #pragma once
 
 #include "hkv_internal.h"
@@ -129,20 +131,13 @@ struct WorkItem {
   int32_t R;     // retained prior rows of head h
 };
 
-// Longest-first order of the heads, this workgroup's (b, h, query tile), and
-// head h's clamped segment starts + exclusive length prefix in LDS.  Ends
-// with a workgroup barrier.  head_rows / head_by_rank need `heads` entries.
+// Retained prior rows of every head (clamped tables) into head_rows[H].
 template <int kThreads>
-__device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_starts,
-                                              const int32_t* __restrict__ seg_ends,
-                                              const int32_t* __restrict__ seg_counts, int64_t cap,
-                                              int H, int S, int B, int32_t n_qt,
-                                              int32_t* head_rows, int32_t* head_by_rank,
-                                              int32_t* seg_start, int32_t* seg_pref) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  for (int hh = tid; hh < H; hh += kThreads) {
+__device__ __forceinline__ void compute_head_rows(const int32_t* __restrict__ seg_starts,
+                                                  const int32_t* __restrict__ seg_ends,
+                                                  const int32_t* __restrict__ seg_counts, int64_t cap,
+                                                  int H, int S, int32_t* head_rows) {
+  for (int hh = threadIdx.x; hh < H; hh += kThreads) {
     int n = seg_counts[hh];
     n = n < 0 ? 0 : (n > S ? S : n);
     int64_t rows = 0;
@@ -155,27 +150,19 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
     }
     head_rows[hh] = static_cast<int32_t>(rows);
   }
-  __syncthreads();
-  for (int hh = tid; hh < H; hh += kThreads) {
-    const int r = head_rows[hh];
-    int rank = 0;
-    for (int o = 0; o < H; ++o) {
-      const int ro = head_rows[o];
-      rank += (ro > r) || (ro == r && o < hh);
-    }
-    head_by_rank[rank] = hh;
-  }
-  __syncthreads();
+}
 
-  WorkItem w;
-  const int32_t per_rank = B * n_qt;
-  const int32_t rank = blockIdx.x / per_rank;
-  const int32_t rem = blockIdx.x - rank * per_rank;
-  w.b = rem / n_qt;
-  w.qt = rem - w.b * n_qt;
-  w.h = head_by_rank[rank];
-  w.bh = w.b * H + w.h;
-
+// Head h's clamped segment starts and exclusive length prefix into LDS (ends
+// with a workgroup barrier); returns the live entry count, w.R = its total.
+template <int kThreads>
+__device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ seg_starts,
+                                                   const int32_t* __restrict__ seg_ends,
+                                                   const int32_t* __restrict__ seg_counts,
+                                                   int64_t cap, int S, WorkItem& w,
+                                                   int32_t* seg_start, int32_t* seg_pref) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   int nseg = seg_counts[w.h];
   nseg = nseg < 0 ? 0 : (nseg > S ? S : nseg);
   for (int i = tid; i < nseg; i += kThreads) {
@@ -214,7 +201,179 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
   __syncthreads();
   w.nseg = nseg;
   w.R = seg_pref[nseg];
+}
+
+// Longest-first order of the heads, the (b, h, query tile) of item `item`
+// in that order, and head h's clamped segment starts + exclusive length
+// prefix in LDS.  Ends with a workgroup barrier.  head_rows / head_by_rank
+// need `heads` entries.  `tab` (tab_ints ints of LDS, free until the
+// return) holds every head's clamped table when 2 H S + H ints fit: then
+// the tables are read from global memory once, all entries in parallel.
+template <int kThreads>
+__device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_starts,
+                                              const int32_t* __restrict__ seg_ends,
+                                              const int32_t* __restrict__ seg_counts, int64_t cap,
+                                              int H, int S, int B, int32_t n_qt,
+                                              int32_t* head_rows, int32_t* head_by_rank,
+                                              int32_t* seg_start, int32_t* seg_pref,
+                                              int32_t item, int32_t* tab, int32_t tab_ints) {
+  const int tid = threadIdx.x;
+  const int32_t HS = H * S;
+  const bool in_lds = 2 * HS + H <= tab_ints;
+  int32_t* const tab_start = tab;
+  int32_t* const tab_len = tab + HS;
+  int32_t* const tab_cnt = tab + 2 * HS;
+  if (in_lds) {
+    for (int idx = tid; idx < HS; idx += kThreads) {
+      int64_t st = seg_starts[idx];
+      int64_t en = seg_ends[idx];
+      st = st < 0 ? 0 : (st > cap ? cap : st);
+      en = en < 0 ? 0 : (en > cap ? cap : en);
+      tab_start[idx] = static_cast<int32_t>(st);
+      tab_len[idx] = en > st ? static_cast<int32_t>(en - st) : 0;
+    }
+    for (int hh = tid; hh < H; hh += kThreads) {
+      const int n = seg_counts[hh];
+      tab_cnt[hh] = n < 0 ? 0 : (n > S ? S : n);
+    }
+    __syncthreads();
+    for (int hh = tid; hh < H; hh += kThreads) {
+      int32_t rows = 0;
+      for (int i = 0; i < tab_cnt[hh]; ++i) rows += tab_len[hh * S + i];
+      head_rows[hh] = rows;
+    }
+  } else {
+    compute_head_rows<kThreads>(seg_starts, seg_ends, seg_counts, cap, H, S, head_rows);
+  }
+  __syncthreads();
+  for (int hh = tid; hh < H; hh += kThreads) {
+    const int r = head_rows[hh];
+    int rank = 0;
+    for (int o = 0; o < H; ++o) {
+      const int ro = head_rows[o];
+      rank += (ro > r) || (ro == r && o < hh);
+    }
+    head_by_rank[rank] = hh;
+  }
+  __syncthreads();
+
+  WorkItem w;
+  const int32_t per_rank = B * n_qt;
+  const int32_t rank = item / per_rank;
+  const int32_t rem = item - rank * per_rank;
+  w.b = rem / n_qt;
+  w.qt = rem - w.b * n_qt;
+  w.h = head_by_rank[rank];
+  w.bh = w.b * H + w.h;
+  if (!in_lds) {
+    load_head_segments<kThreads>(seg_starts, seg_ends, seg_counts, cap, S, w, seg_start, seg_pref);
+    return w;
+  }
+  // head h's entries from the LDS table, then the length prefix (wave 0)
+  const int lane = tid & 63;
+  const int nseg = tab_cnt[w.h];
+  for (int i = tid; i < nseg; i += kThreads) {
+    seg_start[i] = tab_start[w.h * S + i];
+    seg_pref[i + 1] = tab_len[w.h * S + i];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    int v[4];
+    int local = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = lane * 4 + k;
+      v[k] = idx < nseg ? seg_pref[idx + 1] : 0;
+      local += v[k];
+    }
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = lane * 4 + k;
+      run += v[k];
+      if (idx < nseg) seg_pref[idx + 1] = run;
+    }
+    if (lane == 0) seg_pref[0] = 0;
+  }
+  __syncthreads();
+  w.nseg = nseg;
+  w.R = seg_pref[nseg];
   return w;
+}
+
+// ---------------------------------------------------------------- tail split
+//
+// With a workspace, the `tail` = min(items, slots) items dispatched last
+// (the lightest, in longest-first order) are cut into parts of their
+// key-tile stream: the last tail / 4 into 4 parts, the others into 2, so
+// the final wave of work is made of short units that fill the slots evenly.
+// A part leaves its partial result (unnormalized O, running max and sum) in
+// a workspace record; the part that completes an item last merges the
+// records in part order.  Workgroup ids: whole items first, then the 2-part
+// items' parts, then the 4-part items' parts, each item's parts adjacent.
+struct TailSplit {
+  int32_t whole;   // items not cut
+  int32_t two;     // items cut in 2
+  int32_t four;    // items cut in 4
+};
+
+__host__ __device__ __forceinline__ TailSplit tail_split(int32_t items, int32_t slots) {
+  TailSplit t;
+  const int32_t tail = items < slots ? items : slots;
+  t.four = tail / 4;
+  t.two = tail - t.four;
+  t.whole = items - tail;
+  return t;
+}
+
+// Workgroups of a launch, and workspace records / counters it needs.
+__host__ __device__ __forceinline__ int64_t tail_units(const TailSplit& t) {
+  return static_cast<int64_t>(t.whole) + 2LL * t.two + 4LL * t.four;
+}
+__host__ __device__ __forceinline__ int64_t tail_records(const TailSplit& t) {
+  return 2LL * t.two + 4LL * t.four;
+}
+
+struct Unit {
+  int32_t item;     // in longest-first order
+  int32_t part;     // 0 .. parts-1
+  int32_t parts;    // 1, 2 or 4
+  int32_t record;   // first record of the item (parts > 1)
+  int32_t counter;  // counter of the item (parts > 1)
+};
+
+__device__ __forceinline__ Unit tail_unit(const TailSplit& t, int32_t j) {
+  Unit u;
+  if (j < t.whole) {
+    u.item = j;
+    u.part = 0;
+    u.parts = 1;
+    u.record = 0;
+    u.counter = 0;
+    return u;
+  }
+  j -= t.whole;
+  if (j < 2 * t.two) {
+    u.item = t.whole + j / 2;
+    u.part = j % 2;
+    u.parts = 2;
+    u.record = 2 * (j / 2);
+    u.counter = j / 2;
+    return u;
+  }
+  j -= 2 * t.two;
+  u.item = t.whole + t.two + j / 4;
+  u.part = j % 4;
+  u.parts = 4;
+  u.record = 2 * t.two + 4 * (j / 4);
+  u.counter = t.two + j / 4;
+  return u;
 }
 
 // Row table of prior tile `tile` (wave 0, one entry per lane per 64 keys):

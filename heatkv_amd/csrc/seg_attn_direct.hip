@@ -19,8 +19,6 @@
 //    contiguous bytes.
 #include "attn_common.h"
 
-#include <cstdio>
-#include <cstdlib>
 #include <type_traits>
 
 namespace hkv {
@@ -81,9 +79,19 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)(p)));
 }
 
+// Agent-scope relaxed loads and stores of the partial records and counters:
+// coherent across the XCDs' L2 caches without writing back or invalidating
+// them.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int QDT, int KDT, int VDT, int NW, int NS>
 __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
-    const AttnArgs a, const Scalars sc, const int32_t n_qt) {
+    const AttnArgs a, const Scalars sc, const int32_t n_qt, const TailSplit split) {
   static_assert(KDT != kF32 && VDT != kF32 && QDT == KDT, "16-bit inputs only");
   static_assert(NS >= 2 && NS <= 4, "ring depth");
   constexpr int MQK = KDT;
@@ -91,11 +99,13 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
   constexpr int kThreads = NW * 64;
   constexpr int kBM = NW * 32;
   constexpr int kDmaPerWave = kDmaPerTile / NW;
+  static_assert(kPartialFloats == 66 * kThreads, "partial record layout");
 
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStageBytes];
   __shared__ __attribute__((aligned(16))) int32_t rowtab[NS + 1][kBN];
   __shared__ int32_t seg_start[kMaxSegments];
   __shared__ int32_t seg_pref[kMaxSegments + 1];
+  __shared__ int32_t merge_turn;
   static_assert(NS * kStageBytes >= 2 * kMaxHeads * 4, "head tables alias the ring");
 
   const int64_t cap = a.slab_capacity;
@@ -106,15 +116,24 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
   const int g = lane >> 5;
 
-  // The head tables of the work plan live in the (not yet used) ring.
+  // This workgroup's item (longest-first order) and, for a cut item, its
+  // part of the key-tile stream.  The head tables of the plan live in the
+  // not yet used ring.
+  const Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
   int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
   const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
                                          a.max_segments, a.batch, n_qt, head_rows,
-                                         head_rows + kMaxHeads, seg_start, seg_pref);
+                                         head_rows + kMaxHeads, seg_start, seg_pref, un.item,
+                                         head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
   const int32_t R = w.R;
   const int32_t ntp = (R + kBN - 1) / kBN;
   const int32_t ntc = (L + kBN - 1) / kBN;
   const int32_t ntiles = ntp + ntc;
+  // parts of an item with fewer tiles than parts: the surplus parts are empty
+  const int32_t parts = un.parts < ntiles ? un.parts : ntiles;
+  if (un.part >= parts) return;
+  const int32_t t_begin = un.part * ntiles / parts;
+  const int32_t t_end = (un.part + 1) * ntiles / parts;
 
   // Waves issue K or V DMA only: waves [0, 16 / kDmaPerWave) fetch K.
   // Byte ranges are below 2^31 (checked by the C ABI), so a row-table
@@ -172,13 +191,13 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
 
   int cur_seg = 0;
   if (wave == 0) {
-    for (int p = 0; p < NS && p < ntp; ++p)
+    for (int p = t_begin; p < t_begin + NS && p < ntp && p < t_end; ++p)
       fill_rowtab<kD * 2>(p, rowtab[p % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
   }
   __syncthreads();
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p)
-    if (p < ntiles) issue_tile(p);
+    if (t_begin + p < t_end) issue_tile(t_begin + p);
 
   // Q fragments (B operand of S^T = K Q^T): query row, d = 16ks + 8g .. +7
   const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
@@ -199,17 +218,17 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
   float m_run = -1e30f;
   float l_run = 0.f;
 
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = t_begin; t < t_end; ++t) {
     // This wave's DMA for tile t is complete once at most the later tiles'
     // instructions are outstanding (the older Q loads are then complete too).
-    const int later = min(NS - 2, ntiles - 1 - t);
+    const int later = min(NS - 2, t_end - 1 - t);
     if (later <= 0) wait_vmcnt<0>();
     else if (later == 1) wait_vmcnt<kDmaPerWave>();
     else wait_vmcnt<2 * kDmaPerWave>();
     __syncthreads();
     // tile t + NS - 1 reuses the stage of tile t - 1, finished by every wave
-    if (t + NS - 1 < ntiles) issue_tile(t + NS - 1);
-    if (wave == 0 && t + NS < ntp)
+    if (t + NS - 1 < t_end) issue_tile(t + NS - 1);
+    if (wave == 0 && t + NS < ntp && t + NS < t_end)
       fill_rowtab<kD * 2>(t + NS, rowtab[(t + NS) % (NS + 1)], cur_seg, w.nseg, R, seg_start,
                           seg_pref, kPastEnd);
 
@@ -239,50 +258,113 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
     }
   }
   // no DMA is outstanding here: the last tile waited for vmcnt(0)
-  write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  if (parts == 1) {
+    write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+    return;
+  }
+
+  // Part of a cut item: publish the partial record, then count it in.
+  int32_t* const counters = static_cast<int32_t*>(a.workspace);
+  float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
+  float* const rec0 = records + static_cast<int64_t>(un.record) * kPartialFloats;
+  {
+    float* const mine = rec0 + static_cast<int64_t>(un.part) * kPartialFloats;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) st_agent(mine + (db * 16 + j) * kThreads + tid, oacc[db][j]);
+    st_agent(mine + 64 * kThreads + tid, m_run);
+    st_agent(mine + 65 * kThreads + tid, l_run);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (tid == 0)
+    merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+  __syncthreads();
+  if (!merge_turn) return;
+  // Every part is published: combine the parts in part order (this part's
+  // own values from registers, equal to its record), the same arithmetic
+  // whichever part merges.
+  float mp[4], lp[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const bool other = p < parts && p != un.part;
+    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
+    mp[p] = other ? ld_agent(rec + 64 * kThreads + tid) : m_run;
+    lp[p] = other ? ld_agent(rec + 65 * kThreads + tid) : l_run;
+  }
+  float m_new = mp[0];
+#pragma unroll
+  for (int p = 1; p < 4; ++p)
+    if (p < parts) m_new = fmaxf(m_new, mp[p]);
+  f32x16_t acc[4] = {};
+  float l_acc = 0.f;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if (p >= parts) break;
+    const float al = __builtin_amdgcn_exp2f((mp[p] - m_new) * sc.c);
+    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
+    if (p == un.part) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[db][j] = p == 0 ? oacc[db][j] * al : __builtin_fmaf(oacc[db][j], al, acc[db][j]);
+    } else {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float o = ld_agent(rec + (db * 16 + j) * kThreads + tid);
+          acc[db][j] = p == 0 ? o * al : __builtin_fmaf(o, al, acc[db][j]);
+        }
+    }
+    l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
+  }
+  write_output<QDT>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-struct Shape {
-  int nw;
-  int ns;
-};
-
-// Waves per workgroup x ring depth.  HKV_ATTN_DIRECT (read once) selects
-// another compiled shape for tuning sweeps: "4x2" (default: two workgroups
-// per CU), "8x3", "8x4" (one workgroup per CU).
-Shape shape() {
-  static Shape s = [] {
-    Shape r{4, 2};
-    if (const char* e = std::getenv("HKV_ATTN_DIRECT")) {
-      int nw = 0, ns = 0;
-      if (std::sscanf(e, "%dx%d", &nw, &ns) == 2 &&
-          ((nw == 8 && (ns == 3 || ns == 4)) || (nw == 4 && ns == 2)))
-        r = Shape{nw, ns};
-    }
-    return r;
-  }();
-  return s;
+// Resident workgroups of the kernel (2 per CU) on `device`, cached.
+int32_t slots_of(int device) {
+  static int32_t cache[64] = {};
+  if (device < 0 || device >= 64) return 0;
+  if (cache[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+      return 0;
+    cache[device] = 2 * cus < 16384 ? 2 * cus : 16384;  // counters fit kCounterBytes
+  }
+  return cache[device];
 }
 
 template <int DT, int VDT>
 hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
-  const Shape sh = shape();
-  const int32_t bm = sh.nw * 32;
-  const int32_t n_qt = (a.cur_len + bm - 1) / bm;
-  const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
-  if (blocks <= 0) return hipSuccess;
-  if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<uint32_t>(blocks));
-  if (sh.nw == 8 && sh.ns == 4)
-    seg_attn_direct_kernel<DT, DT, VDT, 8, 4><<<grid, 512, 0, st>>>(a, s, n_qt);
-  else if (sh.nw == 8)
-    seg_attn_direct_kernel<DT, DT, VDT, 8, 3><<<grid, 512, 0, st>>>(a, s, n_qt);
-  else
-    seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<grid, 256, 0, st>>>(a, s, n_qt);
+  constexpr int kBM = 128;
+  const int32_t n_qt = (a.cur_len + kBM - 1) / kBM;
+  const int64_t items = static_cast<int64_t>(a.batch) * a.heads * n_qt;
+  if (items <= 0) return hipSuccess;
+  if (items > 0x3fffffffLL) return hipErrorInvalidConfiguration;
+  // With a workspace, the items dispatched last are cut into parts.
+  int device = 0;
+  const int32_t slots = a.workspace != nullptr && hipGetDevice(&device) == hipSuccess ? slots_of(device) : 0;
+  TailSplit split{static_cast<int32_t>(items), 0, 0};
+  if (slots > 0 && a.workspace_bytes >= tail_workspace_bytes(slots)) split = tail_split(static_cast<int32_t>(items), slots);
+  const int64_t blocks = tail_units(split);
+  seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
   return hipGetLastError();
 }
 
 }  // namespace
+
+int32_t tail_slots(int device) { return slots_of(device); }
+
+int64_t tail_workspace_bytes(int32_t slots) {
+  if (slots <= 0) return 0;
+  // counters and records of the largest split: min(items, slots) = slots
+  const TailSplit t = tail_split(slots, slots);
+  return kCounterBytes + tail_records(t) * kPartialFloats * static_cast<int64_t>(sizeof(float));
+}
 
 bool attention_direct_supported(const AttnArgs& a) {
   const bool k16 = a.k_dtype == kBF16 || a.k_dtype == kF16;

@@ -51,7 +51,8 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
 
   const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
                                          a.max_segments, a.batch, n_qt, head_rows, head_by_rank,
-                                         seg_start, seg_pref);
+                                         seg_start, seg_pref, static_cast<int32_t>(blockIdx.x),
+                                         reinterpret_cast<int32_t*>(k_lds), sizeof(k_lds) / 4);
   const int32_t R = w.R;
   const int32_t ntp = (R + kBN - 1) / kBN;
   const int32_t ntc = (L + kBN - 1) / kBN;

@@ -250,6 +250,7 @@ def fused_real_pruning_flat_segmented_attention(
         if return_lse
         else None
     )
+    ws = _lib.attention_workspace(q.device)
     code = _lib.load().hkv_segmented_attention(
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
         segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
@@ -259,6 +260,7 @@ def fused_real_pruning_flat_segmented_attention(
         int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
         _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
         float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
+        ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         _lib.stream_handle(q.device),
     )
     _lib.check(code)
