@@ -417,28 +417,34 @@ __device__ __forceinline__ float pair_sum(float v) {
 }
 
 // Online softmax of one 64-key tile held as S^T blocks (keys 32kb + 8(j>>2) +
-// 4g + (j&3), query = lane & 31).  Overwrites s with p = exp2(c (s - m)),
-// rescales oacc / l_run when the reference max moves.  Keys >= valid_keys
-// get score -inf, hence p = exp2(-inf) = 0 (the launcher guarantees c > 0),
-// so no second mask is needed after the exponentials.
-__device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[4], float& m_run,
-                                             float& l_run, float c, float thresh, int valid_keys,
-                                             int g) {
-  if (valid_keys < kBN) {
-    // key index 32kb + 8(j>>2) + 4g + (j&3) >= valid  <=>  constant >= valid - 4g
-    const int lim = valid_keys - 4 * g;
+// 4g + (j&3), query = lane & 31), in four steps that the pipelined kernel
+// interleaves with matrix work: mask_tile, tile_max, move_max, exp_tile.
+// Keys >= valid_keys get score -inf, hence p = exp2(-inf) = 0 (the launcher
+// guarantees c > 0), so no second mask is needed after the exponentials.
+__device__ __forceinline__ void mask_tile(f32x16_t (&s)[2], int valid_keys, int g) {
+  // key index 32kb + 8(j>>2) + 4g + (j&3) >= valid  <=>  constant >= valid - 4g
+  const int lim = valid_keys - 4 * g;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (kb * 32 + 8 * (j >> 2) + (j & 3) >= lim) s[kb][j] = -__builtin_inff();
-  }
+    for (int j = 0; j < 16; ++j)
+      if (kb * 32 + 8 * (j >> 2) + (j & 3) >= lim) s[kb][j] = -__builtin_inff();
+}
+
+// Row maximum of the tile for the lane's query (both lanes of the pair).
+__device__ __forceinline__ float tile_max(const f32x16_t (&s)[2]) {
   float mx = s[0][0];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[kb][j]);
-  mx = pair_max(mx);
+  return pair_max(mx);
+}
+
+// Moves the reference max (and rescales oacc / l_run) when a row's max grew
+// by more than thresh; lazy, so it rarely runs after the first tiles.
+__device__ __forceinline__ void move_max(f32x16_t (&oacc)[4], float& m_run, float& l_run, float mx,
+                                         float c, float thresh) {
   if (__any(mx - m_run > thresh)) {
     const float m_new = fmaxf(m_run, mx);
     const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
@@ -447,6 +453,10 @@ __device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[
     for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
     m_run = m_new;
   }
+}
+
+// p = exp2(c (s - m)) in place, l_run += sum of p (fp32, unrounded).
+__device__ __forceinline__ void exp_tile(f32x16_t (&s)[2], float m_run, float c, float& l_run) {
   const float mc = m_run * c;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -458,6 +468,14 @@ __device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[
 #pragma unroll
     for (int j = 0; j < 16; ++j) psum[2 * kb + (j >> 3)] += s[kb][j];
   l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
+}
+
+__device__ __forceinline__ void softmax_tile(f32x16_t (&s)[2], f32x16_t (&oacc)[4], float& m_run,
+                                             float& l_run, float c, float thresh, int valid_keys,
+                                             int g) {
+  if (valid_keys < kBN) mask_tile(s, valid_keys, g);
+  move_max(oacc, m_run, l_run, tile_max(s), c, thresh);
+  exp_tile(s, m_run, c, l_run);
 }
 
 // P^T B-operand for PV k-step u (keys 16u + {4g..4g+3, 8+4g..8+4g+3}).

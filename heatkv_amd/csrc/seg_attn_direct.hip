@@ -19,6 +19,8 @@
 //    contiguous bytes.
 #include "attn_common.h"
 
+#include <cstdlib>
+
 #include <type_traits>
 
 namespace hkv {
@@ -87,6 +89,75 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
 }
 __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Part of a cut item: publish the partial record, count it in, and if it is
+// the item's last part to finish, merge every part and write the output.
+template <int QDT, int kThreads>
+__device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc, const Unit& un,
+                                            int32_t parts, const f32x16_t (&oacc)[4], float m_run,
+                                            float l_run, const WorkItem& w, int32_t qrow, int L, int H,
+                                            int g, int32_t& merge_turn) {
+  const int tid = threadIdx.x;
+  int32_t* const counters = static_cast<int32_t*>(a.workspace);
+  float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
+  float* const rec0 = records + static_cast<int64_t>(un.record) * kPartialFloats;
+  {
+    float* const mine = rec0 + static_cast<int64_t>(un.part) * kPartialFloats;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) st_agent(mine + (db * 16 + j) * kThreads + tid, oacc[db][j]);
+    st_agent(mine + 64 * kThreads + tid, m_run);
+    st_agent(mine + 65 * kThreads + tid, l_run);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (tid == 0)
+    merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+  __syncthreads();
+  if (!merge_turn) return;
+  // Every part is published: combine the parts in part order (this part's
+  // own values from registers, equal to its record), the same arithmetic
+  // whichever part merges.
+  float mp[4], lp[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const bool other = p < parts && p != un.part;
+    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
+    mp[p] = other ? ld_agent(rec + 64 * kThreads + tid) : m_run;
+    lp[p] = other ? ld_agent(rec + 65 * kThreads + tid) : l_run;
+  }
+  float m_new = mp[0];
+#pragma unroll
+  for (int p = 1; p < 4; ++p)
+    if (p < parts) m_new = fmaxf(m_new, mp[p]);
+  f32x16_t acc[4] = {};
+  float l_acc = 0.f;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if (p >= parts) break;
+    const float al = __builtin_amdgcn_exp2f((mp[p] - m_new) * sc.c);
+    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
+    if (p == un.part) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[db][j] = p == 0 ? oacc[db][j] * al : __builtin_fmaf(oacc[db][j], al, acc[db][j]);
+    } else {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float o = ld_agent(rec + (db * 16 + j) * kThreads + tid);
+          acc[db][j] = p == 0 ? o * al : __builtin_fmaf(o, al, acc[db][j]);
+        }
+    }
+    l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
+  }
+  write_output<QDT>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int QDT, int KDT, int VDT, int NW, int NS>
@@ -263,66 +334,223 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
     return;
   }
 
-  // Part of a cut item: publish the partial record, then count it in.
-  int32_t* const counters = static_cast<int32_t*>(a.workspace);
-  float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
-  float* const rec0 = records + static_cast<int64_t>(un.record) * kPartialFloats;
-  {
-    float* const mine = rec0 + static_cast<int64_t>(un.part) * kPartialFloats;
+  merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);
+}
+
+// Software-pipelined variant: K runs one tile ahead of V, so iteration t
+// computes S(t+1) = K(t+1) Q^T on the matrix cores while the VALU turns S(t)
+// into P(t) (exponentials, row sums, bf16 pack), then accumulates P(t) V(t)
+// while the VALU takes the row max of S(t+1).  Each wave thus overlaps its
+// own softmax with its own MFMAs instead of relying on the other wave of its
+// SIMD being in the opposite phase.  Same ring (K half of stage t % 2 holds
+// K(t), V half holds V(t)), same row tables (3 slots, filled 3 tiles ahead),
+// one barrier per tile, one tile of DMA in flight per wave.
+template <int QDT, int KDT, int VDT>
+__global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
+    const AttnArgs a, const Scalars sc, const int32_t n_qt, const TailSplit split) {
+  static_assert(KDT != kF32 && VDT != kF32 && QDT == KDT, "16-bit inputs only");
+  constexpr int NW = 4;
+  constexpr int NS = 2;
+  constexpr int MQK = KDT;
+  constexpr int MV = VDT;
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = NW * 32;
+  constexpr int kDmaPerWave = kDmaPerTile / NW;
+  static_assert(kPartialFloats == 66 * kThreads, "partial record layout");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStageBytes];
+  __shared__ __attribute__((aligned(16))) int32_t rowtab[3][kBN];
+  __shared__ int32_t seg_start[kMaxSegments];
+  __shared__ int32_t seg_pref[kMaxSegments + 1];
+  __shared__ int32_t merge_turn;
+  static_assert(NS * kStageBytes >= 2 * kMaxHeads * 4, "head tables alias the ring");
+
+  const int64_t cap = a.slab_capacity;
+  const int H = a.heads;
+  const int L = a.cur_len;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
+  const int g = lane >> 5;
+
+  const Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
+  int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
+  const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
+                                         a.max_segments, a.batch, n_qt, head_rows,
+                                         head_rows + kMaxHeads, seg_start, seg_pref, un.item,
+                                         head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
+  const int32_t R = w.R;
+  const int32_t ntp = (R + kBN - 1) / kBN;
+  const int32_t ntc = (L + kBN - 1) / kBN;
+  const int32_t ntiles = ntp + ntc;
+  const int32_t parts = un.parts < ntiles ? un.parts : ntiles;
+  if (un.part >= parts) return;
+  const int32_t t_begin = un.part * ntiles / parts;
+  const int32_t t_end = (un.part + 1) * ntiles / parts;
+
+  const bool k_wave = wave * kDmaPerWave < 16;
+  const int64_t cur_row0 = static_cast<int64_t>(w.bh) * L;
+  const u32x4_t d_prior = make_desc(
+      static_cast<const uint8_t*>(k_wave ? a.slab_k : a.slab_v) + static_cast<int64_t>(w.b) * cap * kD * 2,
+      static_cast<uint32_t>(cap * kD * 2));
+  const uint8_t* const cur_base =
+      static_cast<const uint8_t*>(k_wave ? a.cur_k : a.cur_v) + cur_row0 * kD * 2;
+  const uint32_t cur_bytes = static_cast<uint32_t>(L * kD * 2);
+  constexpr int32_t kPastEnd = static_cast<int32_t>(0x80000000u);
+
+  int dma_key[kDmaPerWave];
+  int dma_col[kDmaPerWave];
+  int dma_off[kDmaPerWave];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) st_agent(mine + (db * 16 + j) * kThreads + tid, oacc[db][j]);
-    st_agent(mine + 64 * kThreads + tid, m_run);
-    st_agent(mine + 65 * kThreads + tid, l_run);
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    const int q = wave * kDmaPerWave + i;
+    if (k_wave) {
+      dma_key[i] = (q >> 3) * 32 + (lane & 31);
+      dma_col[i] = (q & 7) * 32 + (lane >> 5) * 16;
+    } else {
+      const int qv = q - 16;
+      const int lp = lane & 31;
+      const int db = 2 * (qv & 1) + (lane >> 5);
+      dma_key[i] = 16 * (qv >> 2) + 8 * ((qv >> 1) & 1) + 4 * (lp >> 4) + ((lp & 7) >> 1);
+      dma_col[i] = 2 * (db * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
+    }
+    dma_off[i] = dma_key[i] * (kD * 2) + dma_col[i];
   }
+  const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
+
+  // This wave's tensor (K or V) of tile `tile` into stage tile % 2.
+  auto issue_tile = [&](int tile) {
+    const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
+    if (tile < ntp) {
+      const int32_t* rt = rowtab[tile % 3];
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
+    } else {
+      const uint32_t skip = static_cast<uint32_t>(tile - ntp) * (kBN * kD * 2);
+      const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
+    }
+  };
+  auto valid_of = [&](int t) { return t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN); };
+
+  int cur_seg = 0;
+  if (wave == 0) {
+    for (int p = t_begin; p < t_begin + 3 && p < ntp && p < t_end; ++p)
+      fill_rowtab<kD * 2>(p, rowtab[p % 3], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
+  }
+  __syncthreads();
+  issue_tile(t_begin);
+
+  const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
+  u32x4_t qf[8];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * 2, static_cast<uint32_t>(L * kD * 2));
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
+      qf[ks] ^= sc.q_sign;
+    }
+  }
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
+  float m_run = -1e30f;
+  float l_run = 0.f;
+
+  // S(t) = K(t) Q^T from stage t % 2
+  auto qk = [&](f32x16_t (&sx)[2], int t) {
+    const uint8_t* kst = ring + (t % NS) * kStageBytes + lane * 16;
+    sx[0] = f32x16_t{};
+    sx[1] = f32x16_t{};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kst + (kb * 8 + ks) * 1024);
+        sx[kb] = mfma32<MQK>(kf, qf[ks], sx[kb]);
+      }
+  };
+  // O^T += V(t)^T P(t)^T from stage t % 2
+  auto pv = [&](const u32x4_t (&pf)[4], int t) {
+    const uint8_t* vst = ring + (t % NS) * kStageBytes + kTileBytes + lane * 8;
+#pragma unroll
+    for (int u = 0; u < kBN / 16; ++u)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int blk = (db >> 1) * 1024 + (db & 1) * 512;
+        const u32x2_t lo = ds_read_tr(vst + (u * 4 + 0) * 1024 + blk);
+        const u32x2_t hi = ds_read_tr(vst + (u * 4 + 2) * 1024 + blk);
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[db] = mfma32<MV>(vf, pf[u], oacc[db]);
+      }
+  };
+  auto pack = [&](const f32x16_t (&sx)[2], u32x4_t (&pf)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pf[u] = p_operand<MV>(sx, u);
+  };
+
+  // Prologue: K(t0), V(t0) landed; K(t0 + 1) in flight; S(t0) and its max.
   wait_vmcnt<0>();
   __syncthreads();
-  if (tid == 0)
-    merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
-  __syncthreads();
-  if (!merge_turn) return;
-  // Every part is published: combine the parts in part order (this part's
-  // own values from registers, equal to its record), the same arithmetic
-  // whichever part merges.
-  float mp[4], lp[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const bool other = p < parts && p != un.part;
-    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
-    mp[p] = other ? ld_agent(rec + 64 * kThreads + tid) : m_run;
-    lp[p] = other ? ld_agent(rec + 65 * kThreads + tid) : l_run;
-  }
-  float m_new = mp[0];
-#pragma unroll
-  for (int p = 1; p < 4; ++p)
-    if (p < parts) m_new = fmaxf(m_new, mp[p]);
-  f32x16_t acc[4] = {};
-  float l_acc = 0.f;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    if (p >= parts) break;
-    const float al = __builtin_amdgcn_exp2f((mp[p] - m_new) * sc.c);
-    const float* rec = rec0 + static_cast<int64_t>(p) * kPartialFloats;
-    if (p == un.part) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[db][j] = p == 0 ? oacc[db][j] * al : __builtin_fmaf(oacc[db][j], al, acc[db][j]);
+  if (k_wave && t_begin + 1 < t_end) issue_tile(t_begin + 1);
+  f32x16_t sa[2], sb[2];
+  qk(sa, t_begin);
+  if (valid_of(t_begin) < kBN) mask_tile(sa, valid_of(t_begin), g);
+  move_max(oacc, m_run, l_run, tile_max(sa), sc.c, sc.thresh);
+
+  // Iteration t: scur = S(t) (max applied), snext receives S(t + 1).
+  auto step = [&](f32x16_t (&scur)[2], f32x16_t (&snext)[2], int t) {
+    wait_vmcnt<0>();  // this wave's K(t + 1) or V(t)
+    __syncthreads();
+    if (k_wave) {
+      if (t + 2 < t_end) issue_tile(t + 2);
     } else {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float o = ld_agent(rec + (db * 16 + j) * kThreads + tid);
-          acc[db][j] = p == 0 ? o * al : __builtin_fmaf(o, al, acc[db][j]);
-        }
+      if (t + 1 < t_end) issue_tile(t + 1);
     }
-    l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
+    if (wave == 0 && t + 3 < ntp && t + 3 < t_end)
+      fill_rowtab<kD * 2>(t + 3, rowtab[(t + 3) % 3], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
+    u32x4_t pf[4];
+    qk(snext, t + 1);
+    exp_tile(scur, m_run, sc.c, l_run);
+    pack(scur, pf);
+    pv(pf, t);
+    const int vn = valid_of(t + 1);
+    if (vn < kBN) mask_tile(snext, vn, g);
+    const float mx = tile_max(snext);
+    move_max(oacc, m_run, l_run, mx, sc.c, sc.thresh);
+  };
+  int t = t_begin;
+  for (; t + 2 < t_end; t += 2) {
+    step(sa, sb, t);
+    step(sb, sa, t + 1);
   }
-  write_output<QDT>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
-  if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t + 1 < t_end) {
+    step(sa, sb, t);
+    ++t;
+    // the last tile is in sb
+    wait_vmcnt<0>();
+    __syncthreads();
+    u32x4_t pf[4];
+    exp_tile(sb, m_run, sc.c, l_run);
+    pack(sb, pf);
+    pv(pf, t);
+  } else {
+    wait_vmcnt<0>();
+    __syncthreads();
+    u32x4_t pf[4];
+    exp_tile(sa, m_run, sc.c, l_run);
+    pack(sa, pf);
+    pv(pf, t);
+  }
+
+  if (parts == 1) {
+    write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+    return;
+  }
+  merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);
 }
 
 // Resident workgroups of the kernel (2 per CU) on `device`, cached.
@@ -351,7 +579,11 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   TailSplit split{static_cast<int32_t>(items), 0, 0};
   if (slots > 0 && a.workspace_bytes >= tail_workspace_bytes(slots)) split = tail_split(static_cast<int32_t>(items), slots);
   const int64_t blocks = tail_units(split);
-  seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
+  const char* e = std::getenv("HKV_ATTN_PIPE");
+  if (e == nullptr || e[0] != '0')
+    seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
+  else
+    seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
   return hipGetLastError();
 }
 
