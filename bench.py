@@ -41,7 +41,7 @@ if ROOT not in sys.path:
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BPS = 8.0e12     # MI355X HBM3E
 PROFILES = os.path.join(ROOT, "profiles")
-ATTN_KERNEL = "seg_attn_direct_kernel"
+ATTN_KERNEL = "seg_attn_pipe_kernel"
 
 
 def parse():

@@ -2,7 +2,9 @@
 //
 // K/V tiles move global -> LDS with buffer_load_dwordx4 ... lds (asynchronous,
 // no register staging; rows outside the tensors arrive as zeros) into a ring
-// of NS stages, NS - 1 tiles ahead of the compute, with one barrier per tile.
+// of 2 stages (the K half of stage t % 2 holds K(t), the V half V(t)), one
+// tile ahead of their use, with one barrier per tile; K runs one tile ahead
+// of V (software pipeline, see seg_attn_pipe_kernel).
 //
 // LDS holds each tile in MFMA-operand order, so every operand read is one
 // contiguous 1 KiB (K) or 512 B (V) block per wave at a constant offset:
@@ -18,8 +20,6 @@
 //    instruction fills blocks (2p, u, h) and (2p+1, u, h): 8 key rows x 128
 //    contiguous bytes.
 #include "attn_common.h"
-
-#include <cstdlib>
 
 #include <type_traits>
 
@@ -160,183 +160,6 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int QDT, int KDT, int VDT, int NW, int NS>
-__global__ __launch_bounds__(NW * 64, 2) void seg_attn_direct_kernel(
-    const AttnArgs a, const Scalars sc, const int32_t n_qt, const TailSplit split) {
-  static_assert(KDT != kF32 && VDT != kF32 && QDT == KDT, "16-bit inputs only");
-  static_assert(NS >= 2 && NS <= 4, "ring depth");
-  constexpr int MQK = KDT;
-  constexpr int MV = VDT;
-  constexpr int kThreads = NW * 64;
-  constexpr int kBM = NW * 32;
-  constexpr int kDmaPerWave = kDmaPerTile / NW;
-  static_assert(kPartialFloats == 66 * kThreads, "partial record layout");
-
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * kStageBytes];
-  __shared__ __attribute__((aligned(16))) int32_t rowtab[NS + 1][kBN];
-  __shared__ int32_t seg_start[kMaxSegments];
-  __shared__ int32_t seg_pref[kMaxSegments + 1];
-  __shared__ int32_t merge_turn;
-  static_assert(NS * kStageBytes >= 2 * kMaxHeads * 4, "head tables alias the ring");
-
-  const int64_t cap = a.slab_capacity;
-  const int H = a.heads;
-  const int L = a.cur_len;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
-  const int g = lane >> 5;
-
-  // This workgroup's item (longest-first order) and, for a cut item, its
-  // part of the key-tile stream.  The head tables of the plan live in the
-  // not yet used ring.
-  const Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
-  int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
-  const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
-                                         a.max_segments, a.batch, n_qt, head_rows,
-                                         head_rows + kMaxHeads, seg_start, seg_pref, un.item,
-                                         head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
-  const int32_t R = w.R;
-  const int32_t ntp = (R + kBN - 1) / kBN;
-  const int32_t ntc = (L + kBN - 1) / kBN;
-  const int32_t ntiles = ntp + ntc;
-  // parts of an item with fewer tiles than parts: the surplus parts are empty
-  const int32_t parts = un.parts < ntiles ? un.parts : ntiles;
-  if (un.part >= parts) return;
-  const int32_t t_begin = un.part * ntiles / parts;
-  const int32_t t_end = (un.part + 1) * ntiles / parts;
-
-  // Waves issue K or V DMA only: waves [0, 16 / kDmaPerWave) fetch K.
-  // Byte ranges are below 2^31 (checked by the C ABI), so a row-table
-  // sentinel of 2^31 plus a column offset is past the end of the prior
-  // descriptor and reads zeros.
-  const bool k_wave = wave * kDmaPerWave < 16;
-  const int64_t cur_row0 = static_cast<int64_t>(w.bh) * L;
-  const u32x4_t d_prior = make_desc(
-      static_cast<const uint8_t*>(k_wave ? a.slab_k : a.slab_v) + static_cast<int64_t>(w.b) * cap * kD * 2,
-      static_cast<uint32_t>(cap * kD * 2));
-  const uint8_t* const cur_base =
-      static_cast<const uint8_t*>(k_wave ? a.cur_k : a.cur_v) + cur_row0 * kD * 2;
-  const uint32_t cur_bytes = static_cast<uint32_t>(L * kD * 2);
-  constexpr int32_t kPastEnd = static_cast<int32_t>(0x80000000u);
-
-  // Per-lane key index and byte offset within the key row for each of this
-  // wave's DMA instructions (tile independent), and the byte offset of that
-  // element within a tile of current rows.
-  int dma_key[kDmaPerWave];
-  int dma_col[kDmaPerWave];
-  int dma_off[kDmaPerWave];
-#pragma unroll
-  for (int i = 0; i < kDmaPerWave; ++i) {
-    const int q = wave * kDmaPerWave + i;
-    if (k_wave) {  // K block (kb, ks) = (q / 8, q % 8)
-      dma_key[i] = (q >> 3) * 32 + (lane & 31);
-      dma_col[i] = (q & 7) * 32 + (lane >> 5) * 16;
-    } else {  // V blocks (2p, u, h), (2p + 1, u, h) with q - 16 = (2u + h) * 2 + p
-      const int qv = q - 16;
-      const int lp = lane & 31;
-      const int db = 2 * (qv & 1) + (lane >> 5);
-      dma_key[i] = 16 * (qv >> 2) + 8 * ((qv >> 1) & 1) + 4 * (lp >> 4) + ((lp & 7) >> 1);
-      dma_col[i] = 2 * (db * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
-    }
-    dma_off[i] = dma_key[i] * (kD * 2) + dma_col[i];
-  }
-  const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
-
-  auto issue_tile = [&](int tile) {
-    const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
-    if (tile < ntp) {
-      // rowtab holds slab row * 256 (or the 2^31 sentinel past R)
-      const int32_t* rt = rowtab[tile % (NS + 1)];
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
-    } else {
-      // The descriptor starts at the tile's first row and ends at the last
-      // current row, so rows past L read zeros with no per-lane check.
-      const uint32_t skip = static_cast<uint32_t>(tile - ntp) * (kBN * kD * 2);
-      const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
-    }
-  };
-
-  int cur_seg = 0;
-  if (wave == 0) {
-    for (int p = t_begin; p < t_begin + NS && p < ntp && p < t_end; ++p)
-      fill_rowtab<kD * 2>(p, rowtab[p % (NS + 1)], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int p = 0; p < NS - 1; ++p)
-    if (t_begin + p < t_end) issue_tile(t_begin + p);
-
-  // Q fragments (B operand of S^T = K Q^T): query row, d = 16ks + 8g .. +7
-  const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
-  u32x4_t qf[8];
-  {
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * 2, static_cast<uint32_t>(L * kD * 2));
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
-      qf[ks] ^= sc.q_sign;
-    }
-  }
-
-  f32x16_t oacc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) oacc[i] = f32x16_t{};
-  float m_run = -1e30f;
-  float l_run = 0.f;
-
-  for (int t = t_begin; t < t_end; ++t) {
-    // This wave's DMA for tile t is complete once at most the later tiles'
-    // instructions are outstanding (the older Q loads are then complete too).
-    const int later = min(NS - 2, t_end - 1 - t);
-    if (later <= 0) wait_vmcnt<0>();
-    else if (later == 1) wait_vmcnt<kDmaPerWave>();
-    else wait_vmcnt<2 * kDmaPerWave>();
-    __syncthreads();
-    // tile t + NS - 1 reuses the stage of tile t - 1, finished by every wave
-    if (t + NS - 1 < t_end) issue_tile(t + NS - 1);
-    if (wave == 0 && t + NS < ntp && t + NS < t_end)
-      fill_rowtab<kD * 2>(t + NS, rowtab[(t + NS) % (NS + 1)], cur_seg, w.nseg, R, seg_start,
-                          seg_pref, kPastEnd);
-
-    const uint8_t* kst = ring + (t % NS) * kStageBytes + lane * 16;
-    const uint8_t* vst = ring + (t % NS) * kStageBytes + kTileBytes + lane * 8;
-    f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kst + (kb * 8 + ks) * 1024);
-        s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
-      }
-    const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
-    softmax_tile(s, oacc, m_run, l_run, sc.c, sc.thresh, valid, g);
-#pragma unroll
-    for (int u = 0; u < kBN / 16; ++u) {
-      const u32x4_t pf = p_operand<MV>(s, u);
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int blk = (db >> 1) * 1024 + (db & 1) * 512;
-        const u32x2_t lo = ds_read_tr(vst + (u * 4 + 0) * 1024 + blk);
-        const u32x2_t hi = ds_read_tr(vst + (u * 4 + 2) * 1024 + blk);
-        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = mfma32<MV>(vf, pf, oacc[db]);
-      }
-    }
-  }
-  // no DMA is outstanding here: the last tile waited for vmcnt(0)
-  if (parts == 1) {
-    write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
-    return;
-  }
-
-  merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);
-}
-
 // Software-pipelined variant: K runs one tile ahead of V, so iteration t
 // computes S(t+1) = K(t+1) Q^T on the matrix cores while the VALU turns S(t)
 // into P(t) (exponentials, row sums, bf16 pack), then accumulates P(t) V(t)
@@ -373,7 +196,8 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
   const int g = lane >> 5;
 
-  const Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
+  Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
+  if (split.two == 0 && split.four == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
   int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
   const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
                                          a.max_segments, a.batch, n_qt, head_rows,
@@ -579,11 +403,7 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   TailSplit split{static_cast<int32_t>(items), 0, 0};
   if (slots > 0 && a.workspace_bytes >= tail_workspace_bytes(slots)) split = tail_split(static_cast<int32_t>(items), slots);
   const int64_t blocks = tail_units(split);
-  const char* e = std::getenv("HKV_ATTN_PIPE");
-  if (e == nullptr || e[0] != '0')
-    seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
-  else
-    seg_attn_direct_kernel<DT, DT, VDT, 4, 2><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
+  seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
   return hipGetLastError();
 }
 
