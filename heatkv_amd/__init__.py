@@ -17,5 +17,21 @@ from .slab_schedule import (  # noqa: F401
     build_static_slot_schedule,
     scale_token_ranges,
 )
+from .policy import (  # noqa: F401
+    ScaleSpecificPruningController,
+    pruned_heads_for_budget,
+    strict_pruning_schedule_for_budget_scale_specific,
+    strict_removed_heads_by_scale_specific_for_budget,
+)
+from .enable import (  # noqa: F401
+    METHOD_NAME,
+    canonical_method,
+    enable_real_pruning_scale_specific_fused_segmented,
+)
+from .phase_profile import (  # noqa: F401
+    reset_real_pruning_fast_phase_profile,
+    set_real_pruning_fast_phase_profile_enabled,
+    snapshot_real_pruning_fast_phase_profile,
+)
 
 __version__ = "0.1.0"

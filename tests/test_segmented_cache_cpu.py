@@ -106,3 +106,43 @@ def test_unpruned_policy_stays_dense(cpu_ops):
         cache.step(q, k, v, t, 0.3)
         assert not cache.active
         assert cache.cached_k.shape[2] == sum(s * s for s in sides[:t + 1])
+
+
+def test_generation_flow_under_reference_policy(cpu_ops):
+    """The 13-scale generation of one layer under the reference's HeatKV
+    policy (orders/2b.json, budget 0.1, first source scale 3; pinned by
+    tests/test_policy.py): heads are dropped part-way, freed slab rows are
+    reused by later appends, and every step still equals attention over the
+    keys the policy keeps (head_dim 16 to keep the CPU run short)."""
+    import json
+    import os
+
+    from heatkv_amd import policy as P
+    from heatkv_amd.slab_schedule import SIDES_1M, build_static_slot_schedule
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    orders = json.load(open(os.path.join(here, "golden", "orders_2b.json")))
+    H, layer = 16, 7
+    ctrl = P.controller_for_budget(0.1, orders, num_layers=32, num_heads=H, protected_prefix_scales=3)
+    sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
+    assert any(g.end_target < len(SIDES_1M) for g in sched.segments)  # progressive removal
+    removed = lambda t: ctrl.removed_heads_by_source_for(layer, t)  # noqa: E731
+    cache = sc.SegmentedLayerCache(sched, removed, num_heads=H)
+    inputs = W.generation_inputs(batch=1, heads=H, sides=SIDES_1M, seed=9, dtype=torch.float32, head_dim=16)
+    scale = 0.25
+    for t, (q, k, v) in enumerate(inputs):
+        out = cache.step(q, k, v, t, scale).numpy()
+        rem = removed(t)
+        for h in range(H):
+            srcs = [s for s in range(t) if h not in rem.get(s, set())]
+            kk = torch.cat([inputs[s][1][:, h] for s in srcs] + [k[:, h]], dim=1).numpy()
+            vv = torch.cat([inputs[s][2][:, h] for s in srcs] + [v[:, h]], dim=1).numpy()
+            o, _ = oattn.flat_segmented_attention(
+                q[:, h:h + 1].numpy(), None, None, np.zeros((1, 0), np.int32), np.zeros((1, 0), np.int32),
+                np.zeros(1, np.int32), kk[:, None], vv[:, None], scale)
+            np.testing.assert_allclose(out[:, :, h * 16:(h + 1) * 16], o, rtol=2e-5, atol=2e-5)
+        if cache.active and t + 1 < len(SIDES_1M):
+            for seg in sched.live_segments(t + 1):
+                got = cache.cached_k[:, seg.offset:seg.offset + seg.length]
+                assert torch.equal(got, inputs[seg.source_scale][1][:, seg.head]), (t, seg)
+    assert cache.cached_k is None
