@@ -4,8 +4,10 @@ One step = one ``fused_real_pruning_flat_segmented_attention`` call of the
 final 64x64 scale (B=2, H=16, D=128, 4096 queries, budget-0.1 slab over the
 6425-token prior, seed 1) with its inputs resident in HBM.  The slab is packed
 once before timing (the final scale appends nothing).  ``--warmup`` untimed
-steps, then ``--steps`` back-to-back steps between two HIP events recorded on
-the stream the kernel runs on; prints one JSON line.
+steps (the default 50 covers the GPU's clock ramp from idle: the first ~40
+launches on a fresh box run up to 20 % slower), then ``--steps`` back-to-back
+steps between two HIP events recorded on the stream the kernel runs on;
+prints one JSON line.
 
 * ``value``: attention TFLOP/s over the timed steps, FLOPs counted as
   sum_(b,h) 4 L (R_h + L) D with R_h the retained prior rows (no padding, no
@@ -47,8 +49,8 @@ ATTN_KERNEL = "seg_attn_pipe_kernel"
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5],
                     help="final-step workload (2 = the 2B 1024^2 final scale)")
     ap.add_argument("--budget", type=float, default=None, help="keep budget (configs 1, 2, 4)")

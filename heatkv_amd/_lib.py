@@ -119,12 +119,9 @@ _workspaces: dict = {}
 
 def attention_workspace(device: torch.device):
     """Zero-initialised workspace tensor of ``hkv_segmented_attention`` for the
-    current stream of ``device`` when HKV_ATTN_SPLIT=1 (cut the items
-    dispatched last), else None (every item whole, the default: on the
-    measured workloads the cut items' extra start-up and merge latency cancels
-    the gain in balance).  The kernels leave it zeroed, so it is allocated and
-    cleared once."""
-    if os.environ.get("HKV_ATTN_SPLIT", "0") != "1":
+    current stream of ``device`` (None when HKV_ATTN_SPLIT=0: no item is cut).
+    The kernels leave it zeroed, so it is allocated and cleared once."""
+    if os.environ.get("HKV_ATTN_SPLIT", "1") == "0":
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, torch.cuda.current_stream(idx).cuda_stream)

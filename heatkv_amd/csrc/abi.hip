@@ -144,7 +144,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess)
       return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
-    const int64_t need = hkv::tail_workspace_bytes(hkv::tail_slots(device));
+    const int64_t need = hkv::split_workspace_bytes(hkv::split_slots(device));
     if (need <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
     if (workspace_bytes < need)
       return fail(HKV_ERR_INVALID_ARG, "workspace of %lld bytes is smaller than the %lld required",
@@ -185,7 +185,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
 }
 
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device) {
-  const int64_t need = hkv::tail_workspace_bytes(hkv::tail_slots(device));
+  const int64_t need = hkv::split_workspace_bytes(hkv::split_slots(device));
   if (need <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
   ok();
   return need;

@@ -22,8 +22,9 @@
 //    is moved lazily (only when a row grows by more than 2^8).
 //  * Work items are ordered heaviest head first (longest-processing-time
 //    order); the dispatcher fills free CU slots in workgroup-id order.  The
-//    16-bit kernel can also cut the items dispatched last into parts of
-//    their key-tile stream (tail split, below).
+//    16-bit kernel can also cut some items into two parts of their key-tile
+//    stream so a launch fills whole rounds of the CU slots (round split,
+//    below).
 #pragma once
 
 #include "hkv_internal.h"
@@ -109,6 +110,24 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// 8 fp32 values at byte offset `off` of `r` as two bf16 operands, x = hi +
+// lo + O(2^-18 |x|): hi = x rounded to bf16, lo = (x - hi) rounded to bf16.
+// A product taken as hi*hi + lo*hi + hi*lo then carries about 16 significand
+// bits (TF32 carries 11).  An offset of -1 yields zeros.
+__device__ __forceinline__ void load8_split(__amdgpu_buffer_rsrc_t r, int32_t off, u32x4_t& hi, u32x4_t& lo) {
+  const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  const f32x4_t y = __builtin_bit_cast(
+      f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0));
+  const float v[8] = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = pack2<kBF16>(v[2 * i], v[2 * i + 1]);
+    const float h0 = __builtin_bit_cast(float, hi[i] << 16);
+    const float h1 = __builtin_bit_cast(float, hi[i] & 0xffff0000u);
+    lo[i] = pack2<kBF16>(v[2 * i] - h0, v[2 * i + 1] - h1);
+  }
 }
 
 template <int DT>
@@ -307,72 +326,66 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
   return w;
 }
 
-// ---------------------------------------------------------------- tail split
+// ---------------------------------------------------------------- round split
 //
-// With a workspace, the `tail` = min(items, slots) items dispatched last
-// (the lightest, in longest-first order) are cut into parts of their
-// key-tile stream: the last tail / 4 into 4 parts, the others into 2, so
-// the final wave of work is made of short units that fill the slots evenly.
-// A part leaves its partial result (unnormalized O, running max and sum) in
-// a workspace record; the part that completes an item last merges the
-// records in part order.  Workgroup ids: whole items first, then the 2-part
-// items' parts, then the 4-part items' parts, each item's parts adjacent.
-struct TailSplit {
-  int32_t whole;   // items not cut
-  int32_t two;     // items cut in 2
-  int32_t four;    // items cut in 4
+// With a workspace, some items are cut into two parts of their key-tile
+// stream so that the launch fills whole rounds of the device's resident
+// workgroup slots G: with G < N < 2G items, the last 2G - N (the lightest, in
+// longest-first order) are cut, giving exactly 2G units and a second round
+// that ends with the first instead of one made of a few leftover items; with
+// N <= G, the first min(N, G - N) (the heaviest) are cut, so the one round is
+// not set by the heaviest item.  N >= 2G launches are not cut.  A part
+// leaves its partial result (unnormalized O, running max and sum) in a
+// workspace record; the part that completes an item last merges both records
+// in part order.  Workgroup ids: items [0, first) whole, then the two parts
+// of each cut item (adjacent), then the remaining items whole.
+struct RoundSplit {
+  int32_t items;  // N
+  int32_t first;  // first cut item
+  int32_t two;    // cut items
 };
 
-__host__ __device__ __forceinline__ TailSplit tail_split(int32_t items, int32_t slots) {
-  TailSplit t;
-  const int32_t tail = items < slots ? items : slots;
-  t.four = tail / 4;
-  t.two = tail - t.four;
-  t.whole = items - tail;
+__host__ __device__ __forceinline__ RoundSplit round_split(int32_t items, int32_t slots) {
+  RoundSplit t{items, 0, 0};
+  if (slots <= 0 || items >= 2 * slots) return t;
+  if (items > slots) {
+    t.two = 2 * slots - items;
+    t.first = items - t.two;
+  } else {
+    t.two = items < slots - items ? items : slots - items;
+    t.first = 0;
+  }
   return t;
 }
 
-// Workgroups of a launch, and workspace records / counters it needs.
-__host__ __device__ __forceinline__ int64_t tail_units(const TailSplit& t) {
-  return static_cast<int64_t>(t.whole) + 2LL * t.two + 4LL * t.four;
+// Workgroups of a launch, and workspace records it needs (one counter per
+// cut item, at most G).
+__host__ __device__ __forceinline__ int64_t split_units(const RoundSplit& t) {
+  return static_cast<int64_t>(t.items) + t.two;
 }
-__host__ __device__ __forceinline__ int64_t tail_records(const TailSplit& t) {
-  return 2LL * t.two + 4LL * t.four;
-}
+__host__ __device__ __forceinline__ int64_t split_records(const RoundSplit& t) { return 2LL * t.two; }
 
 struct Unit {
   int32_t item;     // in longest-first order
-  int32_t part;     // 0 .. parts-1
-  int32_t parts;    // 1, 2 or 4
+  int32_t part;     // 0 or 1
+  int32_t parts;    // 1 or 2
   int32_t record;   // first record of the item (parts > 1)
   int32_t counter;  // counter of the item (parts > 1)
 };
 
-__device__ __forceinline__ Unit tail_unit(const TailSplit& t, int32_t j) {
-  Unit u;
-  if (j < t.whole) {
-    u.item = j;
-    u.part = 0;
-    u.parts = 1;
-    u.record = 0;
-    u.counter = 0;
-    return u;
-  }
-  j -= t.whole;
-  if (j < 2 * t.two) {
-    u.item = t.whole + j / 2;
-    u.part = j % 2;
+__device__ __forceinline__ Unit split_unit(const RoundSplit& t, int32_t j) {
+  Unit u{j, 0, 1, 0, 0};
+  if (j < t.first) return u;
+  const int32_t k = j - t.first;
+  if (k < 2 * t.two) {
+    u.item = t.first + k / 2;
+    u.part = k % 2;
     u.parts = 2;
-    u.record = 2 * (j / 2);
-    u.counter = j / 2;
+    u.record = 2 * (k / 2);
+    u.counter = k / 2;
     return u;
   }
-  j -= 2 * t.two;
-  u.item = t.whole + t.two + j / 4;
-  u.part = j % 4;
-  u.parts = 4;
-  u.record = 2 * t.two + 4 * (j / 4);
-  u.counter = t.two + j / 4;
+  u.item = j - t.two;
   return u;
 }
 

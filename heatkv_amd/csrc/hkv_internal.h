@@ -51,20 +51,20 @@ struct AttnArgs {
   int32_t q_dtype;
   int32_t k_dtype;
   int32_t v_dtype;
-  void* workspace;          // tail-split storage, or null
+  void* workspace;          // round-split storage, or null
   int64_t workspace_bytes;
 };
 
 constexpr int kMaxSegments = 256;
 
-// Tail split of the 16-bit attention kernel (workspace layout): kCounterBytes
+// Round split of the 16-bit attention kernel (workspace layout): kCounterBytes
 // of int32 counters (one per cut item, at most one per resident workgroup
-// slot, 2 slots per CU), then partial records of kPartialFloats floats
-// (unnormalized O, running max and sum of 128 queries x 256 threads).
+// slot, 2 slots per CU), then two partial records per slot of kPartialFloats
+// floats (unnormalized O, running max and sum of 128 queries x 256 threads).
 constexpr int kPartialFloats = 66 * 256;
 constexpr int64_t kCounterBytes = 64 * 1024;  // up to 16384 slots
-int32_t tail_slots(int device);  // 0 when the device cannot be queried
-int64_t tail_workspace_bytes(int32_t slots);
+int32_t split_slots(int device);  // 0 when the device cannot be queried
+int64_t split_workspace_bytes(int32_t slots);
 
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream);
 

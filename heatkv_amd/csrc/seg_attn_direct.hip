@@ -170,7 +170,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
 // one barrier per tile, one tile of DMA in flight per wave.
 template <int QDT, int KDT, int VDT>
 __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
-    const AttnArgs a, const Scalars sc, const int32_t n_qt, const TailSplit split) {
+    const AttnArgs a, const Scalars sc, const int32_t n_qt, const RoundSplit split) {
   static_assert(KDT != kF32 && VDT != kF32 && QDT == KDT, "16-bit inputs only");
   constexpr int NW = 4;
   constexpr int NS = 2;
@@ -196,8 +196,8 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
   const int g = lane >> 5;
 
-  Unit un = tail_unit(split, static_cast<int32_t>(blockIdx.x));
-  if (split.two == 0 && split.four == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
+  Unit un = split_unit(split, static_cast<int32_t>(blockIdx.x));
+  if (split.two == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
   int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
   const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
                                          a.max_segments, a.batch, n_qt, head_rows,
@@ -397,25 +397,24 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   const int64_t items = static_cast<int64_t>(a.batch) * a.heads * n_qt;
   if (items <= 0) return hipSuccess;
   if (items > 0x3fffffffLL) return hipErrorInvalidConfiguration;
-  // With a workspace, the items dispatched last are cut into parts.
+  // With a workspace, some items are cut in two so the launch fills whole rounds of slots.
   int device = 0;
   const int32_t slots = a.workspace != nullptr && hipGetDevice(&device) == hipSuccess ? slots_of(device) : 0;
-  TailSplit split{static_cast<int32_t>(items), 0, 0};
-  if (slots > 0 && a.workspace_bytes >= tail_workspace_bytes(slots)) split = tail_split(static_cast<int32_t>(items), slots);
-  const int64_t blocks = tail_units(split);
+  RoundSplit split{static_cast<int32_t>(items), 0, 0};
+  if (slots > 0 && a.workspace_bytes >= split_workspace_bytes(slots)) split = round_split(static_cast<int32_t>(items), slots);
+  const int64_t blocks = split_units(split);
   seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
   return hipGetLastError();
 }
 
 }  // namespace
 
-int32_t tail_slots(int device) { return slots_of(device); }
+int32_t split_slots(int device) { return slots_of(device); }
 
-int64_t tail_workspace_bytes(int32_t slots) {
+int64_t split_workspace_bytes(int32_t slots) {
   if (slots <= 0) return 0;
-  // counters and records of the largest split: min(items, slots) = slots
-  const TailSplit t = tail_split(slots, slots);
-  return kCounterBytes + tail_records(t) * kPartialFloats * static_cast<int64_t>(sizeof(float));
+  // at most one cut item per slot: counters and 2 records per slot
+  return kCounterBytes + 2LL * slots * kPartialFloats * static_cast<int64_t>(sizeof(float));
 }
 
 bool attention_direct_supported(const AttnArgs& a) {

@@ -1,6 +1,10 @@
 // Segmented attention, register-staged variant: serves any mix of fp16 /
-// bf16 / fp32 inputs (fp32 K or V are rounded to bf16 MFMA operands while
-// staging, which the direct-to-LDS variant cannot do).
+// bf16 / fp32 inputs (fp32 K or V are converted to bf16 MFMA operands while
+// staging, which the direct-to-LDS variant cannot do).  fp32 q and k are
+// split into bf16 high and low parts and S = K Q^T is taken as
+// Kh Qh + Kl Qh + Kh Ql (three MFMAs per step, ~16 significand bits, beyond
+// the TF32 products the reference's Triton dot uses for fp32 operands); fp32
+// V and P are rounded to bf16 for O = P V.
 //
 // Each thread loads its share of the next 64-key tile into registers with
 // 16-byte buffer loads (out-of-range rows read as zeros) while the current
@@ -31,9 +35,11 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   constexpr int kEK = KDT == kF32 ? 4 : 2;
   constexpr int kEV = VDT == kF32 ? 4 : 2;
   constexpr int kEQ = QDT == kF32 ? 4 : 2;
+  constexpr bool kSplit = QDT == kF32 && KDT == kF32;
   static_assert(2 * kQuadChunks % kThreads == 0, "loader split");
 
   __shared__ __attribute__((aligned(16))) uint8_t k_lds[kBN * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds_lo[kSplit ? kBN * kKPitch : 16];
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kD * kVtPitch];
   __shared__ __attribute__((aligned(16))) int32_t rowtab[2][kBN];
   __shared__ int32_t seg_start[kMaxSegments];
@@ -74,6 +80,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   // quad-chunk i covers keys 4(i/16)..+3 at d 8(i%16)..+7 of K (i < kQuadChunks)
   // or of V; thread tid owns quad-chunks tid, tid + kThreads, ...
   u32x4_t lreg[kLoadsPerThread][4];
+  u32x4_t lreg_lo[kSplit ? kLoadsPerThread : 1][4];  // low bf16 parts of fp32 K
   auto issue_loads = [&](int tile, int buf) {
     if (tile < ntp) {
 #pragma unroll
@@ -89,6 +96,8 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
         for (int i = 0; i < 4; ++i) {
           if (is_v)
             lreg[it][i] = load8<VDT, MV>(rs_v, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEV);
+          else if constexpr (kSplit)
+            load8_split(rs_k, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEK, lreg[it][i], lreg_lo[it][i]);
           else
             lreg[it][i] = load8<KDT, MQK>(rs_k, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEK);
         }
@@ -107,6 +116,8 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
           const int row = row0 + lq * 4 + i;
           if (is_v)
             lreg[it][i] = load8<VDT, MV>(rc_v, row < L ? (row * kD + lc * 8) * kEV : -1);
+          else if constexpr (kSplit)
+            load8_split(rc_k, row < L ? (row * kD + lc * 8) * kEK : -1, lreg[it][i], lreg_lo[it][i]);
           else
             lreg[it][i] = load8<KDT, MQK>(rc_k, row < L ? (row * kD + lc * 8) * kEK : -1);
         }
@@ -124,8 +135,11 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
       const u32x4_t* r = lreg[it];
       if (!is_v) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
           *reinterpret_cast<u32x4_t*>(k_lds + (lq * 4 + i) * kKPitch + lc * 16) = r[i];
+          if constexpr (kSplit)
+            *reinterpret_cast<u32x4_t*>(k_lds_lo + (lq * 4 + i) * kKPitch + lc * 16) = lreg_lo[it][i];
+        }
       } else {
         // transpose 4 keys x 8 d into 8 rows of V^T (4 keys each)
 #pragma unroll
@@ -146,12 +160,19 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   // Q fragments (B operand of S^T = K Q^T): query row, d = 16ks + 8g .. +7
   const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
   u32x4_t qf[8];
+  u32x4_t qf_lo[kSplit ? 8 : 1];
   {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(
         static_cast<const uint8_t*>(a.q) + cur_row0 * kD * kEQ, static_cast<uint32_t>(L * kD * kEQ));
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * kEQ : -1);
+      const int32_t off = qrow < L ? (qrow * kD + ks * 16 + g * 8) * kEQ : -1;
+      if constexpr (kSplit) {
+        load8_split(rq, off, qf[ks], qf_lo[ks]);
+        qf_lo[ks] ^= sc.q_sign;
+      } else {
+        qf[ks] = load8<QDT, MQK>(rq, off);
+      }
       qf[ks] ^= sc.q_sign;
     }
   }
@@ -183,6 +204,11 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
       for (int kb = 0; kb < 2; ++kb) {
         const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lane + kb * 32 * kKPitch + ks * 32);
         s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
+        if constexpr (kSplit) {
+          const u32x4_t kl = *reinterpret_cast<const u32x4_t*>(k_lane + (k_lds_lo - k_lds) + kb * 32 * kKPitch + ks * 32);
+          s[kb] = mfma32<MQK>(kl, qf[ks], s[kb]);
+          s[kb] = mfma32<MQK>(kf, qf_lo[ks], s[kb]);
+        }
       }
     const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
     softmax_tile(s, oacc, m_run, l_run, sc.c, sc.thresh, valid, g);

@@ -90,14 +90,14 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *   workspace, workspace_bytes : NULL / 0, or device memory of at least
  *              hkv_segmented_attention_workspace_bytes(device) bytes, zeroed
  *              once before its first use (the calls leave it zeroed again).
- *              With it, for 16-bit inputs, the (batch, head, 128-query tile)
- *              items dispatched last (the lightest; at most 2 per CU) are cut
- *              into 2 or 4 parts of their key stream, merged through the
- *              workspace, so the last wave of work fills the device evenly;
- *              without it every item is one workgroup.  Results agree to
- *              rounding; each mode is deterministic.  Calls that may run
- *              concurrently need separate workspaces.  No counterpart in the
- *              reference (its Triton grid is one program per item).
+ *              With it, for 16-bit inputs, a launch with fewer than two
+ *              rounds of (batch, head, 128-query tile) items per resident
+ *              workgroup slot (2 per CU) cuts some items into two halves of
+ *              their key stream, merged through the workspace, so it fills
+ *              whole rounds; without it every item is one workgroup.  Results
+ *              agree to rounding; each mode is deterministic.  Calls that may
+ *              run concurrently need separate workspaces.  No counterpart in
+ *              the reference (its Triton grid is one program per item).
  * head_dim must be 128 and cur_len > 0 (:526-529).  Segment bounds are
  * clamped to [0, slab_capacity) and counts to [0, max_segments], so bad
  * tables cannot address outside the slab.  max_segments <= 256.
@@ -114,8 +114,8 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
 
 /*
  * Bytes of the hkv_segmented_attention workspace for `device` (64 KiB of
- * counters plus 2.5 partial records of 66 KiB per resident workgroup slot,
- * 2 slots per CU: about 87 MB on a 256-CU device); a negative HKV_ERR_*
+ * counters plus 2 partial records of 66 KiB per resident workgroup slot,
+ * 2 slots per CU: about 69 MB on a 256-CU device); a negative HKV_ERR_*
  * code when the device cannot be queried.  No counterpart in the reference.
  */
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device);

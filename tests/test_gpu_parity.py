@@ -178,11 +178,28 @@ def test_attention_dtypes(qk, v, device):
     assert out.dtype == qk
     ref_out, ref_lse = oattn.flat_segmented_attention(
         to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
-    # fp32 q/k are rounded to bf16 MFMA operands; the log-sum-exp then moves by
-    # up to ~1e-2 (the output stays within the contract tolerance)
-    lse_tol = 1e-2 if qk == torch.float32 else 1e-3
-    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, lse_abs=lse_tol,
-                           what=f"{qk}/{v}")
+    # fp32 q/k products are split into bf16 high and low parts (beyond TF32)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"{qk}/{v}")
+
+
+@pytest.mark.parametrize("vdt", [torch.bfloat16, torch.float32])
+def test_attention_fp32_qk_cosine_scores(vdt, device):
+    """fp32 q/k as a cosine-attention model passes them: unit-norm q and k, q
+    scaled by 20..100 per head, softmax scale 1, so scores reach +-100; a bf16
+    rounding of q or k (relative 2^-9) would move them by ~0.2 and the LSE by
+    far more than 1e-3.  Checked against the oracle in fp64."""
+    print(f"[attn] fp32 q/k cosine scores, v={vdt}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(71, 2, 3, 90, 400, 6, dtype=torch.float32,
+                                             kdtype=torch.float32, vdtype=vdt)
+    mul = torch.tensor([20.0, 55.0, 100.0]).view(1, 3, 1, 1)
+    q = torch.nn.functional.normalize(q, dim=-1) * mul
+    ck = torch.nn.functional.normalize(ck, dim=-1)
+    sk = torch.nn.functional.normalize(sk, dim=-1)
+    out, lse = _run(q, sk, sv, tables, ck, cv, 1.0, device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), 1.0,
+        dtype=np.float64)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"cosine fp32 q/k, v={vdt}")
 
 
 def test_attention_no_persisted(device):

@@ -1,12 +1,14 @@
-"""GPU: the tail split of the 16-bit attention kernel.
+"""GPU: the round split of the 16-bit attention kernel.
 
-With a workspace (HKV_ATTN_SPLIT=1 in the Python operator) the (batch, head,
-128-query tile) items dispatched last, min(items, 2 per CU) of them, are cut
-into 2 or 4 parts of their key-tile stream; the part that completes an item
-last merges the parts' partial records.  These cases cover 2- and 4-part
-merges of long and short items, items with fewer tiles than parts, every
-item cut (fewer items than slots), workspace reuse, and determinism, against
-the oracle and against the uncut mode (HKV_ATTN_SPLIT=0, no workspace).
+With a workspace (the Python operator passes one unless HKV_ATTN_SPLIT=0),
+launches with fewer than two rounds of items per CU slot cut some (batch,
+head, 128-query tile) items into two parts of their key-tile stream: the
+lightest ones when there are between one and two rounds, the heaviest when
+there is at most one; the part that completes an item last merges both
+parts' partial records.  These cases cover merges of long and short items,
+items with fewer tiles than parts, every item cut, a second round made of
+cut items, workspace reuse and determinism, against the oracle and against
+the uncut mode (HKV_ATTN_SPLIT=0, no workspace).
 """
 
 from __future__ import annotations
@@ -80,8 +82,8 @@ def test_config2_cut_matches_whole_items(device, monkeypatch):
 
 
 def test_every_item_cut_long_keys(device, monkeypatch):
-    """8 items (fewer than slots): the 2 lightest in 4 parts, the others in 2,
-    each over thousands of retained rows in several segments."""
+    """8 items (fewer than slots): every item cut in two, each over thousands
+    of retained rows in several segments."""
     B, H, L = 1, 8, 128
     cap = 5000 * 8
     print(f"[split] every item cut H={H} cap={cap}", flush=True)
@@ -107,7 +109,7 @@ def test_every_item_cut_long_keys(device, monkeypatch):
 
 @pytest.mark.parametrize("L", [1, 70])
 def test_items_shorter_than_their_parts(device, monkeypatch, L):
-    """Items of one to three tiles cut in 2 or 4 parts: surplus parts are empty."""
+    """Items of one to three tiles cut in two: a part with no tile is empty."""
     B, H, cap, S = 2, 20, 400, 3
     print(f"[split] short items H={H} L={L}", flush=True)
     g = torch.Generator().manual_seed(53 + L)
@@ -124,7 +126,8 @@ def test_items_shorter_than_their_parts(device, monkeypatch, L):
 
 
 def test_items_just_above_slots(device, monkeypatch):
-    """slots + 3 items: 3 whole, the rest cut; heads of mixed retained length."""
+    """slots + 3 items: the 6 heaviest whole, the rest cut in two; heads of
+    mixed retained length."""
     H = _slots(device) + 3
     B, L, cap, S = 1, 100, 3000, 2
     print(f"[split] items just above slots H={H}", flush=True)
@@ -159,3 +162,24 @@ def test_config5_batches_cut(device, monkeypatch):
     o, l = to_np(out), to_np(lse)
     for b in (3, 12):
         assert_attention_close(o[b], l[b], ref_out[b], ref_lse[b], what=f"config 5 b={b}")
+
+
+def test_second_round_of_cut_items(device, monkeypatch):
+    """The 2B shape of scale 11 (L = 2304: 576 items for 512 slots on a 256-CU
+    device): the lightest items are cut so the second round is full."""
+    B, H, L, cap, S = 2, 16, 2304, 6425, 9
+    print(f"[split] second round B={B} H={H} L={L}", flush=True)
+    g = torch.Generator().manual_seed(61)
+    q, ck, cv = (torch.randn((B, H, L, 128), generator=g).to(torch.bfloat16) for _ in range(3))
+    sk = torch.randn((B, cap, 128), generator=g).to(torch.bfloat16)
+    sv = torch.randn((B, cap, 128), generator=g).to(torch.bfloat16)
+    st = torch.randint(0, cap - 600, (H, S), generator=g, dtype=torch.int32)
+    en = st + torch.randint(0, 600, (H, S), generator=g, dtype=torch.int32)
+    ct = torch.randint(0, S + 1, (H,), generator=g, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(128)
+    args = (*_dev(device, q, sk, sv, st, en, ct, ck, cv), scale)
+    cut, whole = _both_modes(monkeypatch, args)
+    rows = [sum(max(0, int(en[h, i]) - int(st[h, i])) for i in range(int(ct[h]))) for h in range(H)]
+    order = sorted(range(H), key=lambda h: (-rows[h], h))
+    heads = sorted({order[0], order[7], order[-1]})
+    _check_vs_oracle(q, sk, sv, st, en, ct, ck, cv, scale, [(cut, "cut"), (whole, "whole")], heads=heads)
