@@ -23,6 +23,9 @@ prints one JSON line.
   SegmentedLayerCache.step (dense-prefix attention, activation pack,
   segmented attention, append), timed per image, plus a phase split from a
   separately profiled image (the profiler synchronizes each phase).
+* ``budgets_8b_class``: the 8B-class final step (B=8, H=32) at keep budgets
+  0.05 / 0.1 / 0.2 / 1.0 (1.0 = every prior token kept, the dense-equivalent
+  case), ms per step and TFLOP/s.
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -57,6 +60,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-repeats", type=int, default=10)
     ap.add_argument("--no-sweep", action="store_true", help="skip the 32-layer generation sweep")
+    ap.add_argument("--no-budgets", action="store_true",
+                    help="skip the 8B-class budget sweep (B=8, H=32, budgets 0.05/0.1/0.2/1.0)")
     ap.add_argument("--sweep-images", type=int, default=3)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
@@ -191,6 +196,29 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
                 copy_bytes_per_image=int(snap["segmented_flat_stats"].get("static_copy_bytes", 0)))
 
 
+def time_budgets(device, steps=20, warmup=10):
+    """The 8B-class final step (B=8, H=32, seed 2) at keep budgets 0.05, 0.1,
+    0.2 and 1.0 (the unpruned, dense-equivalent case): ms per step and TFLOP/s."""
+    import torch
+
+    from heatkv_amd import workloads as W
+
+    base = W.config(4, budget=1.0)
+    out = {}
+    for budget in (0.05, 0.1, 0.2, 1.0):
+        wl = W.with_budget(base, budget)
+        kw = attention_call(wl, device)
+        ms, _ = time_attention(kw, device, steps, warmup)
+        flops = wl.attention_flops()
+        out[str(budget)] = {"ms_per_step": round(ms, 4), "flops_per_step": flops,
+                            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                            "pct_of_bf16_peak": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2),
+                            "slab_capacity": wl.schedule.capacity}
+        del kw
+        torch.cuda.empty_cache()
+    return {"workload": base.name, "batch": base.batch, "heads": base.heads, "budgets": out}
+
+
 def copy_calibration(device, mib):
     """Plain copy of ``mib`` MiB, three launches: reads and writes exactly that many bytes each."""
     import torch
@@ -307,6 +335,8 @@ def main():
     }
     if not args.no_sweep:
         rec["sweep"] = time_sweep(device, args.sweep_images)
+    if not args.no_budgets:
+        rec["budgets_8b_class"] = time_budgets(device)
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(wl, args.cpu_repeats)
     print(json.dumps(rec), flush=True)

@@ -141,6 +141,25 @@ def final_step(*, name: str, batch: int, heads: int, sides=SIDES_1M, budget: flo
                              q, pk, pv, ck, cv, sched, scale)
 
 
+def with_budget(wl: FinalStepWorkload, budget: float,
+                forced_scales: int = FORCED_SCALES) -> FinalStepWorkload:
+    """``wl`` (made by :func:`final_step`) at another keep budget: the same
+    inputs and the same per-(head, scale) uniforms, thresholded at the new
+    keep probability, so the kept sets of increasing budgets are nested."""
+    ranges = scale_token_ranges(wl.sides)
+    n_prior = len(wl.sides) - 1
+    prefix = ranges[n_prior][0]
+    forced_tokens = ranges[min(forced_scales, n_prior) - 1][1] if forced_scales > 0 else 0
+    p = keep_probability(budget, prefix, forced_tokens)
+    gen = torch.Generator().manual_seed(int(wl.seed))
+    u = torch.rand((wl.heads, n_prior), generator=gen, dtype=torch.float64)
+    keep = u < p
+    keep[:, :forced_scales] = True
+    return FinalStepWorkload(wl.name, wl.batch, wl.heads, wl.sides, wl.seed, float(budget), keep,
+                             wl.q, wl.prior_k, wl.prior_v, wl.cur_k, wl.cur_v,
+                             schedule_from_keep(keep, wl.sides), wl.softmax_scale)
+
+
 def skewed_final_step(*, name: str = "skewed_ragged", batch: int = 16, heads: int = 16,
                       sides=SIDES_1M, seed: int = 3, dtype=torch.bfloat16) -> FinalStepWorkload:
     ranges = scale_token_ranges(sides)

@@ -256,3 +256,44 @@ def test_pack_max_length_truncates(device):
     exp = dst.clone()
     exp[:, 10:10 + 64] = src[:, :64]  # 32 * ceil(40 / 32) rows
     assert np.array_equal(bits(dk), bits(exp))
+
+
+_CONFIG4 = []
+
+
+def _config4():
+    if not _CONFIG4:
+        _CONFIG4.append(W.config(4))
+    return _CONFIG4[0]
+
+
+def test_attention_config4_unpruned_equals_dense_sdpa(device):
+    """8B-class shape at budget 1.0: every prior token is kept, so each head's
+    result is dense attention over the whole prefix plus the current scale
+    (the reference's dense path) -- checked with torch SDPA in fp32 on the CPU."""
+    wl = W.with_budget(_config4(), 1.0)
+    print(f"[attn] config 4 budget 1.0 capacity {wl.schedule.capacity}", flush=True)
+    slab_k, slab_v = W.build_slab(wl, device)
+    out, lse = _run(wl.q, slab_k, slab_v, wl.tables(), wl.cur_k, wl.cur_v, wl.softmax_scale, device)
+    o = to_np(out)
+    D = 128
+    b = 5
+    for h in (0, 17, 31):
+        k = torch.cat([wl.prior_k[b, h], wl.cur_k[b, h]], dim=0).float()
+        v = torch.cat([wl.prior_v[b, h], wl.cur_v[b, h]], dim=0).float()
+        q = wl.q[b, h].float()
+        ref = torch.nn.functional.scaled_dot_product_attention(q[None, None], k[None, None], v[None, None],
+                                                               scale=wl.softmax_scale)[0, 0]
+        s = (q @ k.T) * wl.softmax_scale
+        ref_lse = torch.logsumexp(s, dim=-1)
+        assert_attention_close(o[b, :, h * D:(h + 1) * D], to_np(lse)[b, h], ref.numpy(), ref_lse.numpy(),
+                               what=f"config 4 dense b={b} h={h}")
+
+
+def test_attention_config4_budget_005(device):
+    wl = W.with_budget(_config4(), 0.05)
+    r = wl.retained_rows()
+    order = sorted(range(wl.heads), key=lambda h: r[h])
+    heads = sorted({order[0], order[-1]})
+    print(f"[attn] config 4 budget 0.05 heads {heads} R={[r[h] for h in heads]}", flush=True)
+    _check_workload(wl, device, heads=heads, batches=[2])
