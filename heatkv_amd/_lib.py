@@ -125,11 +125,15 @@ def attention_workspace(device: torch.device):
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, torch.cuda.current_stream(idx).cuda_stream)
-    ws = _workspaces.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
+    ws = None if capturing else _workspaces.get(key)
     if ws is None:
         need = int(load().hkv_segmented_attention_workspace_bytes(idx))
         if need < 0:
             check(need)
+        # under HIP-graph capture: a buffer of the graph's own pool, zeroed by a
+        # fill kernel the graph replays (no memset node), not cached
         ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
-        _workspaces[key] = ws
+        if not capturing:
+            _workspaces[key] = ws
     return ws

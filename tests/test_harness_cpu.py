@@ -1,0 +1,35 @@
+"""Host logic of heatkv_amd/harness.py that needs no GPU: method names, the
+seeded removal orders (valid orders for the policy), the result fields."""
+
+from __future__ import annotations
+
+import pytest
+
+from heatkv_amd import harness as Hn
+from heatkv_amd import policy as P
+
+
+def test_method_names_follow_the_reference():
+    assert Hn.normalize_method("baseline") == "baseline"
+    for name in ("real_scale_fused_segmented", "fused-segmented", "fused_segmented"):
+        assert Hn.normalize_method(name) == "real_scale_fused_segmented"
+    with pytest.raises(ValueError, match="unsupported method"):
+        Hn.normalize_method("dense")
+
+
+def test_seeded_orders_are_valid_policy_input():
+    orders = Hn.seeded_orders(32, 16, 9, seed=4)
+    assert orders == Hn.seeded_orders(32, 16, 9, seed=4)
+    norm = P.normalize_orders(orders, num_layers=32, num_heads=16, source_scale_start=3)
+    assert len(norm) == 9 and all(len(o) == 512 for o in norm)
+    ctrl = P.controller_for_budget(0.1, orders, num_layers=32, num_heads=16, protected_prefix_scales=3)
+    assert sum(len(ctrl.removed_heads_for(l, 12, 5)) for l in range(32)) > 0
+
+
+def test_layers_for_each_method():
+    base = Hn.build_layers("baseline", num_layers=2, num_heads=4, budget=0.1, initial_scales=3, orders=None)
+    assert all(not any(l.removed(t) for t in range(13)) for l in base)
+    orders = Hn.seeded_orders(2, 4, 9, seed=1)
+    fused = Hn.build_layers("real_scale_fused_segmented", num_layers=2, num_heads=4, budget=0.1,
+                            initial_scales=3, orders=orders)
+    assert any(l.schedule.capacity < l.schedule.capacity_bound or l.removed(12) for l in fused)
