@@ -184,6 +184,67 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   return ok();
 }
 
+int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bias,
+                        const float* v_bias, const float* scale_mul, const float* rope,
+                        int64_t rope_rows, int64_t rope_start, void* q_out, void* k_out,
+                        void* v_out, void* slab_k, void* slab_v, const int32_t* append_offsets,
+                        int64_t slab_capacity, int32_t batch, int32_t heads, int32_t len,
+                        int32_t head_dim, int32_t qkv_dtype, int32_t q_dtype, int32_t k_dtype,
+                        int32_t v_dtype, int32_t normalize, float eps, void* stream) {
+  if (head_dim != 128) return fail(HKV_ERR_UNSUPPORTED, "qkv producer supports head_dim=128 only");
+  if (qkv_dtype != HKV_DTYPE_BF16 || v_dtype != HKV_DTYPE_BF16)
+    return fail(HKV_ERR_UNSUPPORTED, "qkv producer takes a bfloat16 projection and writes bfloat16 v");
+  if ((q_dtype != HKV_DTYPE_F32 && q_dtype != HKV_DTYPE_BF16) ||
+      (k_dtype != HKV_DTYPE_F32 && k_dtype != HKV_DTYPE_BF16))
+    return fail(HKV_ERR_UNSUPPORTED, "q and k outputs must be float32 or bfloat16");
+  if (batch < 0 || heads <= 0 || len < 0)
+    return fail(HKV_ERR_INVALID_ARG, "batch, len must be >= 0 and heads > 0 (got %d, %d, %d)", batch,
+                len, heads);
+  if (batch == 0 || len == 0) return ok();
+  if (!(eps >= 0.f)) return fail(HKV_ERR_INVALID_ARG, "eps must be >= 0");
+  const int64_t hd = static_cast<int64_t>(heads) * head_dim;
+  if (token_stride < 3 * hd || token_stride % 8 != 0)
+    return fail(HKV_ERR_INVALID_ARG, "token_stride must be >= 3 * heads * head_dim and a multiple of 8");
+  if (!qkv || !q_out || !k_out || !v_out) return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if (rope != nullptr && (rope_start < 0 || rope_rows < rope_start + len))
+    return fail(HKV_ERR_INVALID_ARG, "rope rows [%lld, %lld) outside the table of %lld rows",
+                static_cast<long long>(rope_start), static_cast<long long>(rope_start + len),
+                static_cast<long long>(rope_rows));
+  if (append_offsets != nullptr && (!slab_k || !slab_v || slab_capacity <= 0))
+    return fail(HKV_ERR_INVALID_ARG, "append needs slab_k, slab_v and slab_capacity > 0");
+  // 16-byte vector accesses.
+  const void* aligned[] = {qkv, q_bias, v_bias, rope, q_out, k_out, v_out, slab_k, slab_v};
+  for (const void* p : aligned)
+    if ((reinterpret_cast<uintptr_t>(p) & 15) != 0)
+      return fail(HKV_ERR_INVALID_ARG, "tensor pointers must be 16-byte aligned");
+  hkv::ProduceArgs a{};
+  a.qkv = qkv;
+  a.token_stride = token_stride;
+  a.q_bias = q_bias;
+  a.v_bias = v_bias;
+  a.scale_mul = scale_mul;
+  a.rope = rope;
+  a.rope_rows = rope_rows;
+  a.rope_start = rope_start;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.slab_k = append_offsets != nullptr ? slab_k : nullptr;
+  a.slab_v = append_offsets != nullptr ? slab_v : nullptr;
+  a.append_offsets = append_offsets;
+  a.slab_capacity = slab_capacity;
+  a.rows = static_cast<int64_t>(batch) * len * heads;
+  a.heads = heads;
+  a.len = len;
+  a.q_dtype = q_dtype;
+  a.k_dtype = k_dtype;
+  a.normalize = normalize != 0;
+  a.eps = eps;
+  const hipError_t e = hkv::launch_produce(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HKV_ERR_LAUNCH, "qkv producer launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device) {
   const int64_t need = hkv::split_workspace_bytes(hkv::split_slots(device));
   if (need <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);

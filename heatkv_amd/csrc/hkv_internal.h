@@ -68,4 +68,31 @@ int64_t split_workspace_bytes(int32_t slots);
 
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream);
 
+struct ProduceArgs {
+  const void* qkv;            // bf16 [B, L, 3, H, D], token stride in elements
+  int64_t token_stride;
+  const float* q_bias;        // [H * D] or null
+  const float* v_bias;        // [H * D] or null
+  const float* scale_mul;     // [H] or null
+  const float* rope;          // [2, rope_rows, D / 2] (cos, sin) or null
+  int64_t rope_rows;
+  int64_t rope_start;         // table row of token 0
+  void* q_out;                // [B, H, L, D], q_dtype
+  void* k_out;                // [B, H, L, D], k_dtype
+  void* v_out;                // [B, H, L, D], bf16
+  void* slab_k;               // [B, slab_capacity, D], k_dtype (append) or null
+  void* slab_v;               // [B, slab_capacity, D], bf16
+  const int32_t* append_offsets;  // [H], -1 = head not appended; null = no append
+  int64_t slab_capacity;
+  int64_t rows;               // B * L * H
+  int32_t heads;
+  int32_t len;
+  int32_t q_dtype;
+  int32_t k_dtype;
+  int32_t normalize;
+  float eps;
+};
+
+hipError_t launch_produce(const ProduceArgs& a, hipStream_t stream);
+
 }  // namespace hkv

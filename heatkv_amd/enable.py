@@ -8,8 +8,11 @@ static slab schedule (:func:`heatkv_amd.slab_schedule.build_static_slot_schedule
 and give each layer its segmented KV cache
 (:class:`heatkv_amd.segmented_cache.SegmentedLayerCache`).
 
-What is not here is the model's own attention forward (QKV projection,
-cosine-attention normalization, 2-D RoPE, output projection): the layer calls
+Layers with Infinity's ``SelfAttention`` attributes (``mat_qkv`` ...) also
+get their ``forward`` and ``kv_caching`` replaced, as the reference does
+(:2381-2388), by :mod:`heatkv_amd.attention_forward` (QKV projection, the
+fused HIP producer, the segmented cache step, output projection).  Other
+modules only get the cache: their forward calls
 ``layer.heatkv_cache.step(q, k, v, scale_ind, softmax_scale)`` with its
 post-RoPE ``q, k, v`` ``[B, H, L, D]`` where the reference's patched forward
 runs its cache logic (:2040-2254), and gets the ``[B, L, H * D]`` attention
@@ -18,8 +21,10 @@ output to project.
 
 from __future__ import annotations
 
+import types
 from typing import Callable, List, Optional, Sequence
 
+from .attention_forward import real_scale_fused_segmented_forward, real_scale_fused_segmented_kv_caching
 from .policy import controller_for_budget
 from .segmented_cache import SegmentedLayerCache
 from .slab_schedule import SIDES_1M, build_static_slot_schedule
@@ -59,11 +64,14 @@ def enable_real_pruning_scale_specific_fused_segmented(
     requested_generation_batch_size: Optional[int] = None,
     module_filter: Optional[Callable] = None,
     sides: Sequence[int] = SIDES_1M,
+    patch_forward: bool = True,
 ):
     """Attach the policy, slab schedule and segmented cache to every attention
     layer of ``model`` (same arguments and checks as the reference entry;
     ``module_filter`` selects the layers, by default modules of a class named
-    ``SelfAttention`` with a ``num_heads`` attribute).  Returns ``model``."""
+    ``SelfAttention`` with a ``num_heads`` attribute) and, with
+    ``patch_forward``, replace the forward of layers that have a ``mat_qkv``
+    projection.  Returns ``model``."""
     if merge_mode != "exact":
         raise ValueError("real pruning fast v1 only supports merge_mode='exact'")
     layers = attention_layers(model, module_filter)
@@ -89,4 +97,11 @@ def enable_real_pruning_scale_specific_fused_segmented(
         layer.heatkv_cache = SegmentedLayerCache(
             sched, lambda t, lid=lid: ctrl.removed_heads_by_source_for(lid, t), num_heads=num_heads,
             num_scales=len(sides))
+        if patch_forward and hasattr(layer, "mat_qkv"):
+            if not hasattr(layer, "_pre_heatkv_forward"):
+                layer._pre_heatkv_forward = layer.forward
+            layer.forward = types.MethodType(real_scale_fused_segmented_forward, layer)
+            if not hasattr(layer, "_pre_heatkv_kv_caching"):
+                layer._pre_heatkv_kv_caching = layer.kv_caching
+            layer.kv_caching = types.MethodType(real_scale_fused_segmented_kv_caching, layer)
     return model

@@ -20,7 +20,10 @@ Differences from the reference, all deliberate:
   dot-mode knobs are validated the same way (``ValueError`` on unknown
   values); products always take 16-bit MFMA operands (bf16, or fp16 when the
   inputs are fp16) with fp32 accumulation, which is the reference's default
-  ``bf16`` mode.  fp32 inputs are rounded to bf16 operands.
+  ``bf16`` mode.  fp32 q and k (the cosine-attention model's, whose default
+  mode is a TF32 product) are split into bf16 high and low parts and
+  multiplied as hi*hi + hi*lo + lo*hi, about 16 significand bits; fp32 V and
+  the softmax weights enter the PV product rounded to bf16.
 """
 
 from __future__ import annotations

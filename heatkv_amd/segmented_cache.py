@@ -180,9 +180,29 @@ class SegmentedLayerCache:
 
     # ------------------------------------------------------------------ step
 
+    def producer_append(self, scale_ind: int, k_dtype: torch.dtype, device):
+        """``(slab_k, slab_v, offsets)`` for a producer that appends the kept heads'
+        rows of ``scale_ind`` into the slab before this scale's attention, or
+        None.  Only heads whose slab rows this scale's attention does not read
+        are offered (:meth:`SlabSchedule.fused_append`); the rest stay with the
+        copy after attention.  A step of the same scale must then be called
+        with ``appended=True``."""
+        if (not self.active or self.cached_k is None or scale_ind + 1 >= self.num_scales
+                or self.cached_k.dtype != k_dtype):
+            return None
+        offsets, _ = self.schedule.fused_append(int(scale_ind), device)
+        if offsets is None:
+            return None
+        return self.cached_k, self.cached_v, offsets
+
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale_ind: int,
-             softmax_scale: float, softmax_mode: Optional[str] = None) -> torch.Tensor:
-        """Attention of scale ``scale_ind`` and the cache update for the next scale."""
+             softmax_scale: float, softmax_mode: Optional[str] = None, appended: bool = False) -> torch.Tensor:
+        """Attention of scale ``scale_ind`` and the cache update for the next scale.
+
+        ``appended``: the producer already wrote the rows offered by
+        :meth:`producer_append` for this scale; only the other heads are copied."""
+        if appended and not self.active:
+            raise RuntimeError("appended=True needs an active slab (see producer_append)")
         mode = fused_softmax_mode() if softmax_mode is None else softmax_mode
         final = scale_ind + 1 >= self.num_scales
         old_len = self.logical_len
@@ -247,9 +267,14 @@ class SegmentedLayerCache:
             elif self.active:
                 # append the current scale's kept heads (:969-995)
                 prof.stat_add("static_append_current_calls")
-                plan = self.schedule.append_plans.get((int(scale_ind), int(scale_ind) + 1))
+                if appended:
+                    _, plan = self.schedule.fused_append(int(scale_ind), k.device)
+                    tag = ("append_rest", int(scale_ind))
+                else:
+                    plan = self.schedule.append_plans.get((int(scale_ind), int(scale_ind) + 1))
+                    tag = ("append", int(scale_ind))
                 if plan is not None:
-                    self._copy(plan, k, v, ("append", int(scale_ind)))
+                    self._copy(plan, k, v, tag)
             else:
                 # pack the dense cache and the current scale into a new slab (:1713-1789)
                 dense_k, dense_v = self.cached_k, self.cached_v

@@ -133,6 +133,48 @@ class SlabSchedule:
             self._device_cache[key] = hit
         return hit
 
+    def fused_append(self, scale: int, device) -> Tuple[Optional[torch.Tensor], CopyPlan]:
+        """Split of the append of ``scale`` (plan ``(scale, scale + 1)``) for a
+        producer that writes K/V rows before this scale's attention runs.
+
+        Returns ``(offsets, residual)``: ``offsets`` is an int32 ``[H]`` device
+        tensor with the slab offset of every head whose destination rows lie
+        outside all segments live at ``scale`` (the rows the attention reads),
+        -1 for the others (None when no head qualifies); ``residual`` is the
+        plan of the heads left to the copy after attention.  Cached per
+        (device, scale)."""
+        key = ("fused_append", str(device), int(scale))
+        hit = self._device_cache.get(key)
+        if hit is not None:
+            return hit
+        plan = self.append_plans.get((int(scale), int(scale) + 1))
+        if plan is None or len(plan) == 0:
+            hit = (None, plan if plan is not None else CopyPlan([], [], [], 0))
+            self._device_cache[key] = hit
+            return hit
+        n = plan.sequence_len
+        live = sorted((s.offset, s.offset + s.length) for s in self.live_segments(int(scale)))
+        starts = [a for a, _ in live]
+        offsets = [-1] * self.num_heads
+        rest = []
+        for d, src, ln in zip(plan.dst_starts, plan.src_starts, plan.lengths):
+            whole_head = ln == n and src % n == 0
+            # live segments are disjoint, so the last one starting before
+            # d + ln ends last among them
+            i = bisect.bisect_left(starts, d + ln)
+            clash = i > 0 and live[i - 1][1] > d
+            if whole_head and not clash:
+                offsets[src // n] = d
+            else:
+                rest.append((d, src, ln))
+        residual = CopyPlan([r[0] for r in rest], [r[1] for r in rest], [r[2] for r in rest], n)
+        dev_offsets = None
+        if any(o >= 0 for o in offsets):
+            dev_offsets = torch.tensor(offsets, dtype=torch.int32).to(device)
+        hit = (dev_offsets, residual)
+        self._device_cache[key] = hit
+        return hit
+
     def device_plan(self, plan: CopyPlan, device, tag) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         key = ("plan", str(device), tag)
         hit = self._device_cache.get(key)

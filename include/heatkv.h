@@ -120,6 +120,50 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
  */
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device);
 
+/*
+ * QKV producer epilogue of one scale: from the QKV projection output to the
+ * attention-ready q, k, v, for every (b, l, h):
+ *   x_q, x_k, x_v = qkv[b, l, 0|1|2, h, :] (+ q_bias / v_bias[h*D:(h+1)*D])
+ *   if normalize: x_q /= max(||x_q||, eps); x_k /= max(||x_k||, eps)   (fp32)
+ *   if scale_mul: x_q *= scale_mul[h]
+ *   if rope: pairs (2i, 2i+1) of x_q and x_k rotated with
+ *            c = rope[0, rope_start + l, i], s = rope[1, rope_start + l, i]:
+ *            (c*x0 - s*x1, s*x0 + c*x1), each product and sum rounded
+ *   q_out, k_out, v_out[b, h, l, :] = x_q, x_k, x_v
+ *   if append_offsets and append_offsets[h] >= 0 (and the row fits):
+ *     slab_k, slab_v[b, append_offsets[h] + l, :] = x_k, x_v
+ *
+ * Replaces the prologue of the reference layer forward under bf16 autocast
+ * (enable_real_pruning_fast.py:2040-2072: qkv view/unbind/permute, cosine
+ * attention normalize and scale_mul; apply_rotary_emb,
+ * infinity/models/basic.py:97-117) and, with append_offsets, the append of
+ * the kept heads' current rows into the slab that the reference runs after
+ * attention (enable_real_pruning_fast.py:969-995, 1791-1807).  The append may
+ * only be fused when no slab row it writes is read by this scale's attention.
+ *   qkv : bf16 [batch, len, 3, heads, 128] with token stride token_stride
+ *         elements (>= 3 * heads * 128, multiple of 8)
+ *   q_bias, v_bias : NULL or float32 [heads * 128]; added in fp32 to the bf16
+ *         projection output (the reference adds them before the GEMM output
+ *         is rounded to bf16)
+ *   scale_mul : NULL or float32 [heads] (the exp of the clamped learned scale)
+ *   rope : NULL or float32 [2, rope_rows, 64] (cos table, then sin table);
+ *          rows [rope_start, rope_start + len) are used
+ *   q_out, k_out : [batch, heads, len, 128] of q_dtype / k_dtype (float32 as
+ *          in the reference under autocast, or bfloat16)
+ *   v_out : bf16 [batch, heads, len, 128]
+ *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / bf16
+ *   append_offsets : NULL or int32 [heads] (-1 = head not appended)
+ * All pointers 16-byte aligned.  Rows (b, l, h) with append_offsets[h] + l
+ * outside [0, slab_capacity) are not appended.
+ */
+int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bias,
+                        const float* v_bias, const float* scale_mul, const float* rope,
+                        int64_t rope_rows, int64_t rope_start, void* q_out, void* k_out,
+                        void* v_out, void* slab_k, void* slab_v, const int32_t* append_offsets,
+                        int64_t slab_capacity, int32_t batch, int32_t heads, int32_t len,
+                        int32_t head_dim, int32_t qkv_dtype, int32_t q_dtype, int32_t k_dtype,
+                        int32_t v_dtype, int32_t normalize, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,11 @@ Modules
 ``pack``
     numpy restatement of ``_pack_flat_segments_kv_kernel``
     (real_pruning_fused_attention.py:33-73).
+``produce``
+    numpy restatement of the layer's QKV prologue under bf16 autocast
+    (enable_real_pruning_fast.py:2040-2072: cosine-attention normalize and
+    scale) and of ``apply_rotary_emb`` / ``precompute_rope2d_freqs_grid``
+    (infinity/models/basic.py:39-117).
 
 How each function is pinned (checked against something other than itself) is
 stated in its own docstring; the tests under ``tests/test_oracle_*.py`` hold

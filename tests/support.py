@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 
@@ -34,3 +36,57 @@ def assert_attention_close(out, lse, ref_out, ref_lse, *, max_abs=OUT_MAX_ABS,
         lerr = np.abs(np.asarray(lse, np.float64) - np.asarray(ref_lse, np.float64))
         assert lerr.max() <= lse_abs, f"{what}: lse max-abs {lerr.max():.3e} > {lse_abs}"
     return float(err.max()), float(err.mean())
+
+
+def torch_qkv_prologue(qkv: torch.Tensor, scale_mul: torch.Tensor, table: torch.Tensor, start: int):
+    """The reference layer prologue as torch ops in fp32 on the CPU: ``qkv``
+    ``[B, L, 3, H, D]`` (bf16 values) -> q, k ``[B, H, L, D]`` fp32 and v.
+
+    enable_real_pruning_fast.py:2040-2072 under bf16 autocast (``norm`` runs in
+    fp32 there, so normalize gives fp32) and apply_rotary_emb
+    (infinity/models/basic.py:97-117) with ``table`` ``[2, T, D // 2]``."""
+    import torch.nn.functional as F
+
+    B, L, _, H, D = qkv.shape
+    q, k, v = qkv.float().unbind(dim=2)
+    q = q.permute(0, 2, 1, 3).contiguous()
+    k = k.permute(0, 2, 1, 3).contiguous()
+    v = v.permute(0, 2, 1, 3).contiguous()
+    q = F.normalize(q, dim=-1, eps=1e-12).mul(scale_mul.float().reshape(1, H, 1, 1))
+    k = F.normalize(k, dim=-1, eps=1e-12)
+    rc = table[:, start:start + L]
+    qk = torch.stack((q, k), dim=0).reshape(2, B, H, L, D // 2, 2)
+    qk = torch.stack([rc[0] * qk[..., 0] - rc[1] * qk[..., 1],
+                      rc[1] * qk[..., 0] + rc[0] * qk[..., 1]], dim=-1)
+    q, k = qk.reshape(2, B, H, L, D).unbind(dim=0)
+    return q, k, v
+
+
+class SelfAttention(torch.nn.Module):
+    """A cosine-attention layer with the attributes of Infinity's SelfAttention
+    (infinity/models/basic.py:196-246) that the fused segmented forward reads;
+    random weights, learned-scale values on both sides of the clamp.  Its own
+    forward is never run (the patched forward replaces it)."""
+
+    def __init__(self, embed_dim: int, num_heads: int):
+        super().__init__()
+        self.num_heads, self.head_dim = num_heads, embed_dim // num_heads
+        self.cos_attn, self.scale = True, 1
+        self.scale_mul_1H11 = torch.nn.Parameter(
+            torch.linspace(math.log(4.0), math.log(150.0), num_heads).reshape(1, num_heads, 1, 1))
+        self.max_scale_mul = math.log(100)
+        self.mat_qkv = torch.nn.Linear(embed_dim, 3 * embed_dim, bias=False)
+        self.q_bias = torch.nn.Parameter(torch.randn(embed_dim) * 0.1)
+        self.v_bias = torch.nn.Parameter(torch.randn(embed_dim) * 0.1)
+        self.register_buffer("zero_k_bias", torch.zeros(embed_dim))
+        self.proj = torch.nn.Linear(embed_dim, embed_dim)
+        self.proj_drop = torch.nn.Identity()
+        self.caching = False
+        self.cached_k = self.cached_v = None
+
+    def kv_caching(self, enable: bool):
+        self.caching = enable
+        self.cached_k = self.cached_v = None
+
+    def forward(self, *args, **kwargs):  # pragma: no cover - replaced when enabled
+        raise NotImplementedError("unpatched test layer")

@@ -86,3 +86,26 @@ def test_argument_errors_before_any_device_call():
     # without a device the workspace size cannot be queried
     if not torch.cuda.is_available():
         assert lib.hkv_segmented_attention_workspace_bytes(0) == _lib.HKV_ERR_DEVICE
+
+
+def test_qkv_produce_argument_errors():
+    lib = _lib.load()
+    null = None
+    eps = ctypes.c_float(1e-12)
+
+    def call(**kw):
+        a = dict(qkv=null, stride=3 * 16 * 128, rope=null, rows=0, start=0, append=null, cap=0,
+                 B=1, H=16, L=4, Dh=128, dt_in=2, dt_q=3, dt_k=3, dt_v=2, eps=eps)
+        a.update(kw)
+        return lib.hkv_qkv_produce(a["qkv"], a["stride"], null, null, null, a["rope"], a["rows"], a["start"],
+                                   null, null, null, null, null, a["append"], a["cap"], a["B"], a["H"], a["L"],
+                                   a["Dh"], a["dt_in"], a["dt_q"], a["dt_k"], a["dt_v"], 1, a["eps"], null)
+
+    assert call(Dh=64) == _lib.HKV_ERR_UNSUPPORTED and "head_dim=128" in _lib.last_error()
+    assert call(dt_in=3) == _lib.HKV_ERR_UNSUPPORTED
+    assert call(dt_q=1) == _lib.HKV_ERR_UNSUPPORTED
+    assert call(L=0) == _lib.HKV_OK  # empty scale: nothing to do
+    assert call(H=0) == _lib.HKV_ERR_INVALID_ARG
+    assert call(stride=100) == _lib.HKV_ERR_INVALID_ARG and "token_stride" in _lib.last_error()
+    assert call() == _lib.HKV_ERR_INVALID_ARG and "null" in _lib.last_error()
+    assert call(eps=ctypes.c_float(-1.0)) == _lib.HKV_ERR_INVALID_ARG

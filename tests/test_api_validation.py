@@ -110,3 +110,10 @@ def test_env_knobs(monkeypatch):
     monkeypatch.setenv("REAL_PRUNING_FUSED_VALUE_DOT_MODE", "tf32")
     with pytest.raises(ValueError):
         _fused_value_dot_mode_id()
+
+
+def test_qkv_produce_rejects_cpu_and_non_bf16():
+    from heatkv_amd.produce import qkv_produce
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        qkv_produce(torch.zeros((1, 4, 3 * 2 * 128), dtype=torch.bfloat16), 2)

@@ -146,3 +146,72 @@ def test_generation_flow_under_reference_policy(cpu_ops):
                 got = cache.cached_k[:, seg.offset:seg.offset + seg.length]
                 assert torch.equal(got, inputs[seg.source_scale][1][:, seg.head]), (t, seg)
     assert cache.cached_k is None
+
+
+def test_fused_append_split_under_reference_policy(cpu_ops):
+    """The producer-side append (rows written before the scale's attention)
+    under orders/2b.json at budget 0.1: the split covers the whole append plan,
+    the offered heads never touch a row the attention reads, and a generation
+    that writes them ahead of attention (emulated on the host) equals the
+    retained-key attention and keeps the live slab rows intact."""
+    import json
+    import os
+
+    from heatkv_amd import policy as P
+    from heatkv_amd.slab_schedule import SIDES_1M, build_static_slot_schedule
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    orders = json.load(open(os.path.join(here, "golden", "orders_2b.json")))
+    H = 16
+    ctrl = P.controller_for_budget(0.1, orders, num_layers=32, num_heads=H, protected_prefix_scales=3)
+    offered = 0
+    for layer in range(32):
+        sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
+        for (s, _), plan in sched.append_plans.items():
+            offs, rest = sched.fused_append(s, "cpu")
+            n = plan.sequence_len
+            fused = set()
+            if offs is not None:
+                fused = {(int(o), h * n, n) for h, o in enumerate(offs.tolist()) if o >= 0}
+            items = set(zip(plan.dst_starts, plan.src_starts, plan.lengths))
+            assert fused | set(zip(rest.dst_starts, rest.src_starts, rest.lengths)) == items
+            assert not fused & set(zip(rest.dst_starts, rest.src_starts, rest.lengths))
+            live = [(g.offset, g.offset + g.length) for g in sched.live_segments(s)]
+            for d, _, ln in fused:
+                assert all(d + ln <= a or b <= d for a, b in live), (layer, s, d)
+            offered += len(fused)
+    assert offered > 0
+
+    layer = 29
+    sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
+    removed = lambda t: ctrl.removed_heads_by_source_for(layer, t)  # noqa: E731
+    cache = sc.SegmentedLayerCache(sched, removed, num_heads=H)
+    inputs = W.generation_inputs(batch=1, heads=H, sides=SIDES_1M, seed=5, dtype=torch.float32, head_dim=16)
+    used = 0
+    for t, (q, k, v) in enumerate(inputs):
+        app = cache.producer_append(t, torch.float32, "cpu")
+        if app is not None:
+            slab_k, slab_v, offs = app
+            L = k.shape[2]
+            for h, o in enumerate(offs.tolist()):
+                if o >= 0:
+                    slab_k[:, o:o + L] = k[:, h]
+                    slab_v[:, o:o + L] = v[:, h]
+            used += 1
+        out = cache.step(q, k, v, t, 0.25, appended=app is not None).numpy()
+        rem = removed(t)
+        for h in range(H):
+            srcs = [s for s in range(t) if h not in rem.get(s, set())]
+            kk = torch.cat([inputs[s][1][:, h] for s in srcs] + [k[:, h]], dim=1).numpy()
+            vv = torch.cat([inputs[s][2][:, h] for s in srcs] + [v[:, h]], dim=1).numpy()
+            o, _ = oattn.flat_segmented_attention(
+                q[:, h:h + 1].numpy(), None, None, np.zeros((1, 0), np.int32), np.zeros((1, 0), np.int32),
+                np.zeros(1, np.int32), kk[:, None], vv[:, None], 0.25)
+            np.testing.assert_allclose(out[:, :, h * 16:(h + 1) * 16], o, rtol=2e-5, atol=2e-5)
+        if cache.active and t + 1 < len(SIDES_1M):
+            for seg in sched.live_segments(t + 1):
+                got = cache.cached_k[:, seg.offset:seg.offset + seg.length]
+                assert torch.equal(got, inputs[seg.source_scale][1][:, seg.head]), (t, seg)
+    assert used >= 3
+    with pytest.raises(RuntimeError, match="active slab"):
+        cache.step(*inputs[0], 0, 0.25, appended=True)
