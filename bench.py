@@ -26,6 +26,10 @@ prints one JSON line.
 * ``budgets_8b_class``: the 8B-class final step (B=8, H=32) at keep budgets
   0.05 / 0.1 / 0.2 / 1.0 (1.0 = every prior token kept, the dense-equivalent
   case), ms per step and TFLOP/s.
+* ``producer``: the QKV producer epilogue (normalize, scale_mul, 2-D RoPE,
+  permute; fp32 q/k, bf16 v) of the same final scale against HBM bandwidth:
+  algorithmic bytes = the bf16 projection read + q/k/v written + the scale's
+  RoPE table rows.
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -62,6 +66,7 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true", help="skip the 32-layer generation sweep")
     ap.add_argument("--no-budgets", action="store_true",
                     help="skip the 8B-class budget sweep (B=8, H=32, budgets 0.05/0.1/0.2/1.0)")
+    ap.add_argument("--no-producer", action="store_true", help="skip the QKV producer leg")
     ap.add_argument("--sweep-images", type=int, default=3)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
@@ -194,6 +199,46 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
                 phase_gpu_ms_profiled={k: round(v, 3) for k, v in snap["cuda_ms"].items()},
                 phase_calls=snap["calls"],
                 copy_bytes_per_image=int(snap["segmented_flat_stats"].get("static_copy_bytes", 0)))
+
+
+def time_producer(device, batch=2, heads=16, reps=100, warmup=20):
+    """QKV producer of the final 64x64 scale (L=4096) from a bf16 projection:
+    average duration, algorithmic bytes and bandwidth."""
+    import torch
+
+    from heatkv_amd import produce as P
+    from heatkv_amd.slab_schedule import SIDES_1M
+
+    sched = [(1, s, s) for s in SIDES_1M]
+    L, D = SIDES_1M[-1] ** 2, 128
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn((batch, L, 3 * heads * D), generator=g).to(torch.bfloat16).to(device)
+    sm = (torch.rand(heads, generator=g) * 4.6).exp().to(device)
+    table = P.rope2d_freqs_table(D, sched, 2, 128).to(device)
+    start = P.rope_start(sched, len(sched) - 1)
+
+    def run():
+        return P.qkv_produce(qkv, heads, scale_mul=sm, rope_table=table, rope_start_row=start)
+
+    for _ in range(warmup):
+        run()
+    stream = torch.cuda.current_stream(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    t0.record(stream)
+    for _ in range(reps):
+        run()
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    ms = t0.elapsed_time(t1) / reps
+    elems = batch * L * heads * D
+    nbytes = elems * 2 * 3 + elems * (4 + 4 + 2) + 2 * L * (D // 2) * 4
+    return {"what": f"QKV producer, final scale (B={batch}, L={L}, H={heads}), fp32 q/k, bf16 v",
+            "kernel": "produce_kernel", "us": round(ms * 1e3, 2), "bytes": nbytes,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
+            "traffic": measured_traffic("produce_kernel", "2b_final_1024")}
 
 
 def time_budgets(device, steps=20, warmup=10):
@@ -333,6 +378,8 @@ def main():
             "frac_hbm": round(pack_bytes / (pack_ms * 1e-3) / PEAK_HBM_BPS, 4),
         },
     }
+    if not args.no_producer:
+        rec["producer"] = time_producer(device)
     if not args.no_sweep:
         rec["sweep"] = time_sweep(device, args.sweep_images)
     if not args.no_budgets:
