@@ -30,6 +30,10 @@ prints one JSON line.
   permute; fp32 q/k, bf16 v) of the same final scale against HBM bandwidth:
   algorithmic bytes = the bf16 projection read + q/k/v written + the scale's
   RoPE table rows.
+* ``real_model``: the same final step as the cosine-attention model runs it
+  under bf16 autocast: fp32 unit-norm k (slab and current), fp32 q scaled
+  by 30, bf16 v, softmax scale 1 (the staged kernel, split-bf16 q/k
+  products), with the nominal FLOP count.
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -67,6 +71,7 @@ def parse():
     ap.add_argument("--no-budgets", action="store_true",
                     help="skip the 8B-class budget sweep (B=8, H=32, budgets 0.05/0.1/0.2/1.0)")
     ap.add_argument("--no-producer", action="store_true", help="skip the QKV producer leg")
+    ap.add_argument("--no-real-model", action="store_true", help="skip the fp32 q/k (model precision) leg")
     ap.add_argument("--sweep-images", type=int, default=3)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
@@ -234,11 +239,47 @@ def time_producer(device, batch=2, heads=16, reps=100, warmup=20):
     ms = t0.elapsed_time(t1) / reps
     elems = batch * L * heads * D
     nbytes = elems * 2 * 3 + elems * (4 + 4 + 2) + 2 * L * (D // 2) * 4
+    # practical HBM ceiling for comparison: a plain device copy of the same size
+    src = torch.empty(nbytes // 2, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize(device)
+    c0 = torch.cuda.Event(enable_timing=True)
+    c1 = torch.cuda.Event(enable_timing=True)
+    c0.record(stream)
+    for _ in range(20):
+        dst.copy_(src)
+    c1.record(stream)
+    torch.cuda.synchronize(device)
+    copy_gbs = 2 * src.numel() / (c0.elapsed_time(c1) / 20 * 1e-3) / 1e9
+    del src, dst
     return {"what": f"QKV producer, final scale (B={batch}, L={L}, H={heads}), fp32 q/k, bf16 v",
             "kernel": "produce_kernel", "us": round(ms * 1e3, 2), "bytes": nbytes,
             "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (ms * 1e-3) / PEAK_HBM_BPS, 4),
-            "traffic": measured_traffic("produce_kernel", "2b_final_1024")}
+            "traffic": measured_traffic("produce_kernel", "2b_final_1024"),
+            "copy_GB/s_same_bytes": round(copy_gbs, 1)}
+
+
+def time_real_model(device, steps=50, warmup=20):
+    """Final 2B step at the model's precision: fp32 q/k, bf16 v, scale 1."""
+    import torch
+    import torch.nn.functional as F
+
+    from heatkv_amd import workloads as W
+
+    wl = W.config(2)
+    kw = attention_call(wl, device)
+    kw["q"] = F.normalize(kw["q"].float(), dim=-1) * 30.0
+    kw["current_k"] = F.normalize(kw["current_k"].float(), dim=-1)
+    kw["persisted_k"] = F.normalize(kw["persisted_k"].float().nan_to_num(0.0), dim=-1)
+    kw["softmax_scale"] = 1.0
+    ms, _ = time_attention(kw, device, steps, warmup)
+    flops = wl.attention_flops()
+    return {"what": "2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 (staged kernel)",
+            "ms_per_step": round(ms, 4), "tflops_nominal": round(flops / (ms * 1e-3) / 1e12, 1),
+            "pct_of_bf16_peak_nominal": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2)}
 
 
 def time_budgets(device, steps=20, warmup=10):
@@ -380,6 +421,8 @@ def main():
     }
     if not args.no_producer:
         rec["producer"] = time_producer(device)
+    if not args.no_real_model:
+        rec["real_model"] = time_real_model(device)
     if not args.no_sweep:
         rec["sweep"] = time_sweep(device, args.sweep_images)
     if not args.no_budgets:
