@@ -33,7 +33,8 @@ prints one JSON line.
 * ``real_model``: the same final step as the cosine-attention model runs it
   under bf16 autocast: fp32 unit-norm k (slab and current), fp32 q scaled
   by 30, bf16 v, softmax scale 1 (the staged kernel, split-bf16 q/k
-  products), with the nominal FLOP count.
+  products), with the nominal FLOP count; ``tf32_mode``: the same step with
+  q and k in fp16 (TF32's significand, REAL_PRUNING_FUSED_QK_DOT_MODE=tf32).
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -276,10 +277,15 @@ def time_real_model(device, steps=50, warmup=20):
     kw["persisted_k"] = F.normalize(kw["persisted_k"].float().nan_to_num(0.0), dim=-1)
     kw["softmax_scale"] = 1.0
     ms, _ = time_attention(kw, device, steps, warmup)
+    for name in ("q", "current_k", "persisted_k"):
+        kw[name] = kw[name].half()
+    ms16, _ = time_attention(kw, device, steps, warmup)
     flops = wl.attention_flops()
     return {"what": "2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 (staged kernel)",
             "ms_per_step": round(ms, 4), "tflops_nominal": round(flops / (ms * 1e-3) / 1e12, 1),
-            "pct_of_bf16_peak_nominal": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2)}
+            "pct_of_bf16_peak_nominal": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2),
+            "tf32_mode": {"what": "same step, q/k in fp16 (16-bit kernel)", "ms_per_step": round(ms16, 4),
+                          "tflops": round(flops / (ms16 * 1e-3) / 1e12, 1)}}
 
 
 def time_budgets(device, steps=20, warmup=10):

@@ -27,7 +27,12 @@ Precision: the reference runs its dense-prefix scales through the model's own
 flash attention with q and k cast to bf16 (basic.py:296-302) and its
 segmented scales with fp32 q and k (a TF32 product); here every scale attends
 with the fp32 q and k of the producer (split-bf16 products, about 16
-significand bits).
+significand bits).  With ``REAL_PRUNING_FUSED_QK_DOT_MODE=tf32`` (the
+reference's knob for TF32 q/k products) a cosine-attention layer's producer
+writes q and k as fp16 instead: the same 11-bit significand as TF32, exact
+range for cosine attention (|k| = 1, |q| <= exp(max_scale_mul)), half the K
+cache, and the 16-bit attention kernel (one product per MFMA step instead of
+three).
 """
 
 from __future__ import annotations
@@ -36,6 +41,9 @@ import torch
 import torch.nn.functional as F
 
 from .produce import qkv_produce, rope_start, rope_table_for, scale_mul_of
+from .real_pruning_fused_attention import _fused_qk_dot_mode_id
+
+_QK_DOT_TF32 = 1
 
 
 def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, attn_fn=None,
@@ -59,8 +67,11 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
         start = rope_start(scale_schedule, scale_ind)
     cos_attn = bool(self.cos_attn)
     # q and k are fp32 wherever the reference promotes them (cosine attention
-    # or RoPE); otherwise they stay bf16 as in the reference.
+    # or RoPE); otherwise they stay bf16 as in the reference.  TF32 dot mode
+    # on a cosine-attention layer: fp16 (TF32's significand, values in range).
     qk_dtype = torch.float32 if (cos_attn or table is not None) else torch.bfloat16
+    if cos_attn and _fused_qk_dot_mode_id() == _QK_DOT_TF32:
+        qk_dtype = torch.float16
     cache = self.heatkv_cache
     append = cache.producer_append(int(scale_ind), qk_dtype, qkv.device)
     q, k, v = qkv_produce(

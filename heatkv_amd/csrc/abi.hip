@@ -194,9 +194,8 @@ int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bi
   if (head_dim != 128) return fail(HKV_ERR_UNSUPPORTED, "qkv producer supports head_dim=128 only");
   if (qkv_dtype != HKV_DTYPE_BF16 || v_dtype != HKV_DTYPE_BF16)
     return fail(HKV_ERR_UNSUPPORTED, "qkv producer takes a bfloat16 projection and writes bfloat16 v");
-  if ((q_dtype != HKV_DTYPE_F32 && q_dtype != HKV_DTYPE_BF16) ||
-      (k_dtype != HKV_DTYPE_F32 && k_dtype != HKV_DTYPE_BF16))
-    return fail(HKV_ERR_UNSUPPORTED, "q and k outputs must be float32 or bfloat16");
+  if (elem_bytes(q_dtype) == 0 || q_dtype != k_dtype)
+    return fail(HKV_ERR_UNSUPPORTED, "q and k outputs must share one dtype: float32, float16 or bfloat16");
   if (batch < 0 || heads <= 0 || len < 0)
     return fail(HKV_ERR_INVALID_ARG, "batch, len must be >= 0 and heads > 0 (got %d, %d, %d)", batch,
                 len, heads);

@@ -47,6 +47,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void unpack_bf16x8(u32x4_t w, float (&x)[kPer]) {
 #pragma unroll
@@ -62,12 +63,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// Round to nearest even; out-of-range values become +-inf.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+}
+
 template <int DT>
 __device__ __forceinline__ void store_row8(void* base, int64_t elem, const float (&x)[kPer]) {
   if constexpr (DT == kF32) {
     f32x4_t* p = reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + elem);
     p[0] = f32x4_t{x[0], x[1], x[2], x[3]};
     p[1] = f32x4_t{x[4], x[5], x[6], x[7]};
+  } else if constexpr (DT == kF16) {
+    u32x4_t w = {pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]), pack_f16x2(x[4], x[5]),
+                 pack_f16x2(x[6], x[7])};
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(base) + elem) = w;
   } else {
     u32x4_t w = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]),
                  pack_bf16x2(x[6], x[7])};
@@ -118,7 +129,7 @@ __device__ __forceinline__ void rotate(float (&x)[kPer], f32x4_t c, f32x4_t s) {
   }
 }
 
-template <int QT, int KT>
+template <int QT, int KT = QT>
 __global__ __launch_bounds__(kThreads) void produce_kernel(ProduceArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
   const int j = threadIdx.x % kLanes;
@@ -190,11 +201,13 @@ hipError_t launch_produce(const ProduceArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<uint32_t>(blocks));
-  const bool q32 = a.q_dtype == kF32, k32 = a.k_dtype == kF32;
-  if (q32 && k32) produce_kernel<kF32, kF32><<<grid, kThreads, 0, stream>>>(a);
-  else if (q32) produce_kernel<kF32, kBF16><<<grid, kThreads, 0, stream>>>(a);
-  else if (k32) produce_kernel<kBF16, kF32><<<grid, kThreads, 0, stream>>>(a);
-  else produce_kernel<kBF16, kBF16><<<grid, kThreads, 0, stream>>>(a);
+  if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
+  switch (a.q_dtype) {
+    case kF32: produce_kernel<kF32><<<grid, kThreads, 0, stream>>>(a); break;
+    case kF16: produce_kernel<kF16><<<grid, kThreads, 0, stream>>>(a); break;
+    case kBF16: produce_kernel<kBF16><<<grid, kThreads, 0, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

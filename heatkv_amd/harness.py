@@ -18,6 +18,14 @@ CFG pair per image).  Methods:
   (HIP pack + segmented attention), as
   ``enable_real_pruning_scale_specific_fused_segmented`` sets it up.
 
+``--layer-forward`` times whole attention layers instead: per layer a
+cosine-attention module with Infinity ``SelfAttention``'s parameters (random
+bf16 weights, ``--embed-dim`` 2048 for the 2B model) whose forward the enable
+entry replaces (QKV projection, HIP producer, segmented cache step, output
+projection), the layers chained within each scale step, one random input per
+scale.  ``baseline`` is then the same forward with nothing pruned (budget 1,
+the dense cache of every scale).
+
 ``--graph`` captures one whole generation (all layer-steps) in a HIP graph
 after an eager warm-up run and times replays.  Usage::
 
@@ -38,8 +46,9 @@ from typing import Iterable, List, Optional
 import torch
 
 from . import phase_profile as prof
-from .enable import METHOD_ALIASES, METHOD_NAME
+from .enable import METHOD_ALIASES, METHOD_NAME, enable_real_pruning_scale_specific_fused_segmented
 from .policy import controller_for_budget, load_orders
+from .produce import precompute_rope2d_freqs_grid
 from .segmented_cache import SegmentedLayerCache
 from .slab_schedule import SIDES_1M, build_slab_schedule, build_static_slot_schedule, scale_token_ranges
 from .workloads import generation_inputs
@@ -85,27 +94,81 @@ def build_layers(method: str, *, num_layers: int, num_heads: int, budget: float,
     return layers
 
 
+class SyntheticSelfAttention(torch.nn.Module):
+    """Cosine-attention layer with the parameters and attributes of Infinity's
+    ``SelfAttention`` (infinity/models/basic.py:196-246), randomly initialized
+    from ``seed``; learned scales spread over [log 4, log 100].  Its own
+    forward is never used: the enable entry replaces it."""
+
+    def __init__(self, embed_dim: int, num_heads: int, seed: int):
+        super().__init__()
+        gen = torch.Generator().manual_seed(int(seed))
+        self.num_heads, self.head_dim = int(num_heads), int(embed_dim) // int(num_heads)
+        self.cos_attn, self.scale, self.caching = True, 1, False
+        self.max_scale_mul = math.log(100)
+        self.scale_mul_1H11 = torch.nn.Parameter(
+            torch.linspace(math.log(4.0), math.log(100.0), num_heads).reshape(1, num_heads, 1, 1))
+        bound = 1.0 / math.sqrt(embed_dim)
+        self.mat_qkv = torch.nn.Linear(embed_dim, 3 * embed_dim, bias=False)
+        self.proj = torch.nn.Linear(embed_dim, embed_dim)
+        with torch.no_grad():
+            self.mat_qkv.weight.uniform_(-bound, bound, generator=gen)
+            self.proj.weight.uniform_(-bound, bound, generator=gen)
+            self.proj.bias.uniform_(-bound, bound, generator=gen)
+        self.q_bias = torch.nn.Parameter(torch.randn(embed_dim, generator=gen) * 0.02)
+        self.v_bias = torch.nn.Parameter(torch.randn(embed_dim, generator=gen) * 0.02)
+        self.register_buffer("zero_k_bias", torch.zeros(embed_dim))
+        self.proj_drop = torch.nn.Identity()
+        self.cached_k = self.cached_v = None
+
+    def kv_caching(self, enable: bool):
+        self.caching = bool(enable)
+        self.cached_k = self.cached_v = None
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError("enable_real_pruning_scale_specific_fused_segmented replaces this forward")
+
+
+def build_model(method: str, *, device, num_layers: int, num_heads: int, embed_dim: int, budget: float,
+                initial_scales: int, orders, seed: int = 0) -> torch.nn.ModuleList:
+    """Chained synthetic attention layers (bf16) with the fused segmented path
+    enabled; ``baseline`` enables it at budget 1 (nothing pruned)."""
+    model = torch.nn.ModuleList([SyntheticSelfAttention(embed_dim, num_heads, seed * 1000 + l)
+                                 for l in range(num_layers)])
+    model = model.to(device=device, dtype=torch.bfloat16)
+    return enable_real_pruning_scale_specific_fused_segmented(
+        model, 1.0 if method == BASELINE else budget, orders, protected_prefix_scales=initial_scales,
+        source_scale_start=initial_scales,
+        module_filter=lambda m: isinstance(m, SyntheticSelfAttention))
+
+
 def profile_one(method: str, batch_size: int, *, device, num_layers: int = 32, num_heads: int = 16,
                 budget: float = 0.1, initial_scales: int = 3, orders=None, seed: int = 0, warmup: int = 1,
-                repeats: int = 2, phase_profile: bool = True, graph: bool = False) -> dict:
+                repeats: int = 2, phase_profile: bool = True, graph: bool = False,
+                layer_forward: bool = False, embed_dim: int = 2048) -> dict:
     """One (method, batch size) result with the reference harness's fields."""
     method = normalize_method(method)
     if orders is None:
         orders = seeded_orders(num_layers, num_heads, 12 - initial_scales, seed)
-    layers = build_layers(method, num_layers=num_layers, num_heads=num_heads, budget=budget,
-                          initial_scales=initial_scales, orders=orders)
     B = 2 * int(batch_size)  # CFG pair per image
-    inputs = [generation_inputs(batch=B, heads=num_heads, sides=SIDES_1M, seed=seed * 1000 + l, device=device)
-              for l in range(num_layers)]
-    scale = 1.0 / math.sqrt(128)
     sink: List[torch.Tensor] = []
+    if layer_forward:
+        generation = _layer_generation(method, B, sink, device=device, num_layers=num_layers,
+                                       num_heads=num_heads, embed_dim=embed_dim, budget=budget,
+                                       initial_scales=initial_scales, orders=orders, seed=seed)
+    else:
+        layers = build_layers(method, num_layers=num_layers, num_heads=num_heads, budget=budget,
+                              initial_scales=initial_scales, orders=orders)
+        inputs = [generation_inputs(batch=B, heads=num_heads, sides=SIDES_1M, seed=seed * 1000 + l,
+                                    device=device) for l in range(num_layers)]
+        scale = 1.0 / math.sqrt(128)
 
-    def generation():
-        sink.clear()
-        for t in range(len(SIDES_1M)):
-            for l in range(num_layers):
-                q, k, v = inputs[l][t]
-                sink.append(layers[l].step(q, k, v, t, scale))
+        def generation():
+            sink.clear()
+            for t in range(len(SIDES_1M)):
+                for l in range(num_layers):
+                    q, k, v = inputs[l][t]
+                    sink.append(layers[l].step(q, k, v, t, scale))
 
     use_prof = phase_profile and method == METHOD_NAME and not graph
     g = None
@@ -156,7 +219,37 @@ def profile_one(method: str, batch_size: int, *, device, num_layers: int = 32, n
         "peak_reserved_bytes": max(peak_res) if peak_res else 0,
         "phase_profiles": phases,
         "graph": bool(graph),
+        "layer_forward": bool(layer_forward),
     }
+
+
+def _layer_generation(method, B, sink, *, device, num_layers, num_heads, embed_dim, budget, initial_scales,
+                      orders, seed):
+    """A generation of chained synthetic attention layers (patched forward
+    under bf16 autocast): returns the callable that runs one image."""
+    model = build_model(method, device=device, num_layers=num_layers, num_heads=num_heads,
+                        embed_dim=embed_dim, budget=budget, initial_scales=initial_scales, orders=orders,
+                        seed=seed)
+    sched = [(1, s, s) for s in SIDES_1M]
+    grid = precompute_rope2d_freqs_grid(embed_dim // num_heads, {1.0: {"1M": {"scales": sched}}}, 2,
+                                        pad_to_multiplier=128, device=device)
+    gen = torch.Generator().manual_seed(int(seed))
+    xs = [torch.randn((B, s * s, embed_dim), generator=gen).to(device=device, dtype=torch.bfloat16)
+          for s in SIDES_1M]
+
+    @torch.no_grad()
+    def generation():
+        sink.clear()
+        for layer in model:
+            layer.kv_caching(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for t in range(len(SIDES_1M)):
+                x = xs[t]
+                for layer in model:
+                    x = layer(x, None, None, sched, grid, t)
+                sink.append(x)
+
+    return generation
 
 
 def main(argv: Optional[Iterable[str]] = None) -> int:
@@ -174,6 +267,9 @@ def main(argv: Optional[Iterable[str]] = None) -> int:
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--heads", type=int, default=16)
     ap.add_argument("--graph", action="store_true", help="time HIP-graph replays of a whole generation")
+    ap.add_argument("--layer-forward", action="store_true",
+                    help="time whole attention layers (QKV projection, producer, cache step, projection)")
+    ap.add_argument("--embed-dim", type=int, default=2048)
     ap.add_argument("--json-out", type=str, default=None)
     args = ap.parse_args(argv)
     if args.warmup < 0 or args.repeats <= 0:
@@ -186,7 +282,8 @@ def main(argv: Optional[Iterable[str]] = None) -> int:
             res = profile_one(method, batch_size, device=device, num_layers=args.layers, num_heads=args.heads,
                               budget=args.head_specific_budget, initial_scales=args.head_specific_initial_scales,
                               orders=orders, seed=args.seed, warmup=args.warmup, repeats=args.repeats,
-                              phase_profile=not args.disable_phase_profile, graph=args.graph)
+                              phase_profile=not args.disable_phase_profile, graph=args.graph,
+                              layer_forward=args.layer_forward, embed_dim=args.embed_dim)
             results.append(res)
             print(f"{res['method']} b{batch_size}: median={res['median_ms']:.1f} ms "
                   f"per_image={res['per_image_median_ms']:.1f} ms "
@@ -203,7 +300,10 @@ def main(argv: Optional[Iterable[str]] = None) -> int:
             "head_specific_budget": args.head_specific_budget,
             "head_specific_initial_scales": args.head_specific_initial_scales,
             "graph": args.graph,
-            "data": "synthetic per-layer q/k/v (2B shape); attention + cache update only",
+            "layer_forward": args.layer_forward,
+            "data": ("synthetic inputs, random bf16 weights; attention layers (projections, producer, "
+                     "attention, cache update)" if args.layer_forward else
+                     "synthetic per-layer q/k/v (2B shape); attention + cache update only"),
         },
         "results": results,
     }

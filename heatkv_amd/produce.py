@@ -172,7 +172,10 @@ def qkv_produce(
       k's / v's dtype and int32 ``[H]`` device offsets (-1 = not appended):
       rows of head h also go to ``slab[b, offsets[h] + l]``.
 
-    q, k are ``qk_dtype`` (fp32 like the reference, or bf16), v bf16.
+    q, k are ``qk_dtype``: fp32 like the reference, fp16 (the 11-bit
+    significand of the TF32 products the reference's attention takes of fp32
+    q/k, for values within fp16's range, e.g. cosine attention's), or bf16;
+    v is bf16.
     """
     if not qkv.is_cuda:
         raise RuntimeError("qkv_produce runs on the GPU only (HIP kernel); got a CPU tensor")
@@ -191,8 +194,8 @@ def qkv_produce(
             raise ValueError(f"qkv last dim must be 3 * heads * {D} = {3 * H * D} (got {qkv.shape[2]})")
     else:
         raise ValueError("qkv must be [B, L, 3*H*D] or [B, L, 3, H, D]")
-    if qk_dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError("qk_dtype must be torch.float32 or torch.bfloat16")
+    if qk_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("qk_dtype must be torch.float32, torch.float16 or torch.bfloat16")
     qkv = qkv.contiguous()
     dev = qkv.device
     _lib.require_device(dev)

@@ -148,8 +148,10 @@ int64_t hkv_segmented_attention_workspace_bytes(int32_t device);
  *   scale_mul : NULL or float32 [heads] (the exp of the clamped learned scale)
  *   rope : NULL or float32 [2, rope_rows, 64] (cos table, then sin table);
  *          rows [rope_start, rope_start + len) are used
- *   q_out, k_out : [batch, heads, len, 128] of q_dtype / k_dtype (float32 as
- *          in the reference under autocast, or bfloat16)
+ *   q_out, k_out : [batch, heads, len, 128] of q_dtype == k_dtype: float32
+ *          (the reference's values under autocast), float16 (the same
+ *          11-bit significand as the TF32 products the reference's attention
+ *          takes of fp32 q/k; elements beyond +-65504 become inf) or bfloat16
  *   v_out : bf16 [batch, heads, len, 128]
  *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / bf16
  *   append_offsets : NULL or int32 [heads] (-1 = head not appended)

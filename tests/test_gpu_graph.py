@@ -52,3 +52,33 @@ def test_graph_replays_match_eager(device, method):
         generation()  # eager work between replays
         torch.cuda.synchronize(device)
         assert all(np.array_equal(bits(o), w) for o, w in zip(sink, want))
+
+
+@pytest.mark.parametrize("method", ["real_scale_fused_segmented", "baseline"])
+def test_layer_forward_graph_replays_match_eager(device, method):
+    """Whole attention layers (QKV projection, HIP producer with the fused
+    append, cache step, output projection) of a 13-scale generation, two
+    chained 2B-shaped layers, captured in one HIP graph."""
+    L, H = 2, 16
+    orders = Hn.seeded_orders(L, H, 9, seed=4)
+    sink = []
+    generation = Hn._layer_generation(method, 2, sink, device=device, num_layers=L, num_heads=H,
+                                      embed_dim=2048, budget=0.1, initial_scales=3, orders=orders, seed=5)
+    print(f"[layer graph] {method}: eager reference", flush=True)
+    generation()
+    torch.cuda.synchronize(device)
+    want = [bits(o) for o in sink]
+    assert all(np.isfinite(o.float().cpu().numpy()).all() for o in sink)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        generation()
+    outs = list(sink)
+    for rep in range(3):
+        print(f"[layer graph] {method}: replay {rep}", flush=True)
+        g.replay()
+        torch.cuda.synchronize(device)
+        for i, (o, w) in enumerate(zip(outs, want)):
+            assert np.array_equal(bits(o), w), (rep, i)
+        generation()
+        torch.cuda.synchronize(device)
+        assert all(np.array_equal(bits(o), w) for o, w in zip(sink, want))

@@ -112,6 +112,15 @@ def test_producer_bias_no_normalize_and_bf16_out(device):
         g32 = to_np(got.float())
         assert np.mean(g32 != O.bf16_round(want)) < 1e-3
         assert np.all(np.abs(g32 - want) <= np.abs(want) * 2.0 ** -8 + atol)
+    # fp16 q/k outputs (TF32's significand): one fp16 rounding (2^-11 relative)
+    q, k, _ = P.qkv_produce(qkv.to(device), H, scale_mul=sm.to(device), rope_table=table.to(device),
+                            rope_start_row=start, qk_dtype=torch.float16)
+    assert q.dtype == k.dtype == torch.float16
+    for got, want, atol in ((q, wq, 4e-6 * sm.numpy()[None, :, None, None]), (k, wk, 4e-6)):
+        g32 = to_np(got.float())
+        assert np.mean(g32 != want.astype(np.float16).astype(np.float32)) < 1e-3
+        # 2^-11 relative rounding, or half the subnormal spacing 2^-25 below 2^-14
+        assert np.all(np.abs(g32 - want) <= np.abs(want) * 2.0 ** -11 + 2.0 ** -25 + atol)
 
 
 def test_producer_zero_rows_5d_input_and_empty(device):
@@ -185,14 +194,17 @@ def test_generation_with_fused_append_matches_unfused(device):
     assert n_fused >= 3
 
 
-@pytest.mark.parametrize("budget", [1.0, 0.3])
+@pytest.mark.parametrize("budget,qk_mode", [(1.0, "bf16"), (0.3, "bf16"), (0.3, "tf32")])
 @torch.no_grad()
-def test_patched_layer_forward(device, budget):
+def test_patched_layer_forward(device, budget, qk_mode, monkeypatch):
     """Two cosine-attention layers (H=4, C=512) through a 13-scale generation
     with the patched forward under bf16 autocast; per layer and step, the
     attention output entering proj against fp32 attention over the oracle's
     q/k/v of the same projection output and the policy's kept keys (scales
-    of 1600+ tokens: batch row 1 and heads 0 and 3)."""
+    of 1600+ tokens: batch row 1 and heads 0 and 3).  In TF32 dot mode the
+    producer writes fp16 q/k, and the oracle attends over q and k rounded to
+    fp16 (TF32's significand)."""
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", qk_mode)
     H, B, start_scale = 4, 2, 3
     torch.manual_seed(0)
     model = torch.nn.ModuleList([SelfAttention(512, H) for _ in range(2)]).to(device)
@@ -225,6 +237,10 @@ def test_patched_layer_forward(device, budget):
             arr = qkv.float().cpu().numpy().reshape(B, L, 3, H, D)
             sm = (layer.scale_mul_1H11.reshape(-1).float().clamp_max(layer.max_scale_mul).exp()).cpu().numpy()
             q, k, v = O.produce(arr, scale_mul=sm, table=table, start=P.rope_start(SCHED_1M, t))
+            if qk_mode == "tf32":
+                q = q.astype(np.float16).astype(np.float32)
+                k = k.astype(np.float16).astype(np.float32)
+                assert layer.heatkv_cache.cached_k is None or layer.heatkv_cache.cached_k.dtype == torch.float16
             hist[li].append((k, v))
             rem = ctrl.removed_heads_by_source_for(li, t)
             removed_any |= any(len(s) > 0 for s in rem.values())

@@ -4,6 +4,7 @@ seeded removal orders (valid orders for the policy), the result fields."""
 from __future__ import annotations
 
 import pytest
+import torch
 
 from heatkv_amd import harness as Hn
 from heatkv_amd import policy as P
@@ -33,3 +34,20 @@ def test_layers_for_each_method():
     fused = Hn.build_layers("real_scale_fused_segmented", num_layers=2, num_heads=4, budget=0.1,
                             initial_scales=3, orders=orders)
     assert any(l.schedule.capacity < l.schedule.capacity_bound or l.removed(12) for l in fused)
+
+
+def test_synthetic_layers_get_the_patched_forward():
+    from heatkv_amd.attention_forward import real_scale_fused_segmented_forward
+
+    orders = Hn.seeded_orders(2, 4, 9, seed=1)
+    model = Hn.build_model("real_scale_fused_segmented", device="cpu", num_layers=2, num_heads=4, embed_dim=512,
+                          budget=0.2, initial_scales=3, orders=orders)
+    for i, layer in enumerate(model):
+        assert layer.layer_idx == i and layer.forward.__func__ is real_scale_fused_segmented_forward
+        assert layer.mat_qkv.weight.dtype == torch.bfloat16
+        layer.kv_caching(True)
+        assert layer.caching and layer.heatkv_cache.logical_len == 0
+    base = Hn.build_model("baseline", device="cpu", num_layers=2, num_heads=4, embed_dim=512, budget=0.2,
+                         initial_scales=3, orders=orders)
+    ctrl = base[0].heatkv_controller
+    assert all(not any(ctrl.removed_heads_by_source_for(l, t).values()) for l in range(2) for t in range(13))
