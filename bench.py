@@ -35,6 +35,10 @@ prints one JSON line.
   by 30, bf16 v, softmax scale 1 (the staged kernel, split-bf16 q/k
   products), with the nominal FLOP count; ``tf32_mode``: the same step with
   q and k in fp16 (TF32's significand, REAL_PRUNING_FUSED_QK_DOT_MODE=tf32).
+* ``measured_peaks``: what this device reaches on plain library work in the
+  same run: a bf16 8192^3 GEMM (torch.matmul, hipBLASLt) in TFLOP/s and a
+  1 GiB device copy in GB/s (read + write), beside the nominal 2.5 PF / 8 TB/s;
+  ``attention_frac_of_gemm`` relates the attention to the former.
 * ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
   softmax, restated) on the host cores over whole steps, rank 0 only.
 """
@@ -73,6 +77,7 @@ def parse():
                     help="skip the 8B-class budget sweep (B=8, H=32, budgets 0.05/0.1/0.2/1.0)")
     ap.add_argument("--no-producer", action="store_true", help="skip the QKV producer leg")
     ap.add_argument("--no-real-model", action="store_true", help="skip the fp32 q/k (model precision) leg")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured GEMM / copy peaks")
     ap.add_argument("--sweep-images", type=int, default=3)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
@@ -288,6 +293,42 @@ def time_real_model(device, steps=50, warmup=20):
                           "tflops": round(flops / (ms16 * 1e-3) / 1e12, 1)}}
 
 
+def _events_ms(fn, device, reps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream(device)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    t0.record(stream)
+    for _ in range(reps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    return t0.elapsed_time(t1) / reps
+
+
+def measured_peaks(device):
+    """bf16 GEMM TFLOP/s and device-copy GB/s reached on this device."""
+    import torch
+
+    n = 8192
+    a = torch.randn((n, n), device=device, dtype=torch.bfloat16)
+    b = torch.randn((n, n), device=device, dtype=torch.bfloat16)
+    ms_mm = _events_ms(lambda: torch.matmul(a, b), device, 20, 10)
+    del a, b
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    ms_cp = _events_ms(lambda: dst.copy_(src), device, 20, 5)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bf16_gemm_8192_tflops": round(2 * n ** 3 / (ms_mm * 1e-3) / 1e12, 1),
+            "copy_1gib_GBps": round(2 * (1 << 30) / (ms_cp * 1e-3) / 1e9, 1),
+            "nominal_bf16_tflops": PEAK_BF16_FLOPS / 1e12, "nominal_hbm_GBps": PEAK_HBM_BPS / 1e9}
+
+
 def time_budgets(device, steps=20, warmup=10):
     """The 8B-class final step (B=8, H=32, seed 2) at keep budgets 0.05, 0.1,
     0.2 and 1.0 (the unpruned, dense-equivalent case): ms per step and TFLOP/s."""
@@ -353,7 +394,30 @@ def cpu_baseline(wl, repeats):
         oattn.flat_segmented_attention(*args)
         times.append(time.perf_counter() - t)
     sec = statistics.median(times)
+    from heatkv_amd import workloads as W
+
+    w1 = W.config(1)
+    st1, en1, ct1 = (t.numpy() for t in w1.tables())
+    s1_k = np.zeros((w1.batch, w1.schedule.capacity, 128), np.float32)
+    s1_v = np.zeros_like(s1_k)
+    for seg in w1.schedule.live_segments(w1.target):
+        s1_k[:, seg.offset:seg.offset + seg.length] = f(w1.prior_k)[:, seg.head, seg.scale_start:seg.scale_end]
+        s1_v[:, seg.offset:seg.offset + seg.length] = f(w1.prior_v)[:, seg.head, seg.scale_start:seg.scale_end]
+    args1 = (f(w1.q), s1_k, s1_v, st1, en1, ct1, f(w1.cur_k), f(w1.cur_v), w1.softmax_scale)
+    oattn.flat_segmented_attention(*args1)
+    t1 = []
+    for _ in range(5):
+        t = time.perf_counter()
+        oattn.flat_segmented_attention(*args1)
+        t1.append(time.perf_counter() - t)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), model)
+    except OSError:
+        pass
     return dict(value=round(wl.attention_flops() / sec / 1e12, 4), unit="TFLOP/s", cores=threads,
+                cpu_model=model, config1_ms_per_step=round(statistics.median(t1) * 1e3, 3),
                 kind="port",
                 sample=f"{repeats} whole steps of {wl.name} (B={wl.batch}, H={wl.heads}, "
                        f"L={wl.cur_len}), numpy fp32 oracle, median",
@@ -433,6 +497,9 @@ def main():
         rec["sweep"] = time_sweep(device, args.sweep_images)
     if not args.no_budgets:
         rec["budgets_8b_class"] = time_budgets(device)
+    if not args.no_peaks:
+        rec["measured_peaks"] = measured_peaks(device)
+        rec["attention_frac_of_gemm"] = round(achieved / 1e12 / rec["measured_peaks"]["bf16_gemm_8192_tflops"], 4)
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(wl, args.cpu_repeats)
     print(json.dumps(rec), flush=True)
