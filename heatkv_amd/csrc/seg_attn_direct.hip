@@ -207,7 +207,12 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const int32_t ntp = (R + kBN - 1) / kBN;
   const int32_t ntc = (L + kBN - 1) / kBN;
   const int32_t ntiles = ntp + ntc;
-  const int32_t parts = un.parts < ntiles ? un.parts : ntiles;
+  // A part needs kMinPartTiles key tiles to pay for its record and the
+  // merge, so a short item runs as fewer parts (one, below two such runs);
+  // every part of the item sees the same tile count and agrees.  Parts past
+  // the count leave at once.
+  int32_t parts = ntiles / kMinPartTiles;
+  parts = parts < 1 ? 1 : (parts < un.parts ? parts : un.parts);
   if (un.part >= parts) return;
   const int32_t t_begin = un.part * ntiles / parts;
   const int32_t t_end = (un.part + 1) * ntiles / parts;
@@ -400,8 +405,9 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   // With a workspace, some items are cut in two so the launch fills whole rounds of slots.
   int device = 0;
   const int32_t slots = a.workspace != nullptr && hipGetDevice(&device) == hipSuccess ? slots_of(device) : 0;
-  RoundSplit split{static_cast<int32_t>(items), 0, 0};
-  if (slots > 0 && a.workspace_bytes >= split_workspace_bytes(slots)) split = round_split(static_cast<int32_t>(items), slots);
+  RoundSplit split{static_cast<int32_t>(items), 0, 0, 0};
+  if (slots > 0 && a.workspace_bytes >= split_workspace_bytes(slots))
+    split = round_split(static_cast<int32_t>(items), slots, (a.cur_len + kBN - 1) / kBN);
   const int64_t blocks = split_units(split);
   seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
   return hipGetLastError();

@@ -5,10 +5,14 @@ launches with fewer than two rounds of items per CU slot cut some (batch,
 head, 128-query tile) items into two parts of their key-tile stream: the
 lightest ones when there are between one and two rounds, the heaviest when
 there is at most one; the part that completes an item last merges both
-parts' partial records.  These cases cover merges of long and short items,
-items with fewer tiles than parts, every item cut, a second round made of
-cut items, workspace reuse and determinism, against the oracle and against
-the uncut mode (HKV_ATTN_SPLIT=0, no workspace).
+parts' partial records.  An item with fewer than 16 key tiles runs whole
+(its second part leaves at once).  The parts of a cut item are adjacent
+workgroups when the current scale alone gives every item 16 tiles, else all
+first parts precede all second parts.  These cases cover merges of long and
+short items, short items whose second part leaves, every item cut (grouped
+parts), a mix of cut and whole-running items, a second round made of cut
+items (adjacent parts), workspace reuse and determinism, against the oracle
+and against the uncut mode (HKV_ATTN_SPLIT=0, no workspace).
 """
 
 from __future__ import annotations
@@ -109,7 +113,8 @@ def test_every_item_cut_long_keys(device, monkeypatch):
 
 @pytest.mark.parametrize("L", [1, 70])
 def test_items_shorter_than_their_parts(device, monkeypatch, L):
-    """Items of one to three tiles cut in two: a part with no tile is empty."""
+    """Items of one to three tiles: too short for two parts, so the second
+    part of each leaves and the first runs the item whole."""
     B, H, cap, S = 2, 20, 400, 3
     print(f"[split] short items H={H} L={L}", flush=True)
     g = torch.Generator().manual_seed(53 + L)
