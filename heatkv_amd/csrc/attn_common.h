@@ -481,6 +481,8 @@ __device__ __forceinline__ void mask_tile(f32x16_t (&s)[2], int valid_keys, int 
 }
 
 // Row maximum of the tile for the lane's query (both lanes of the pair).
+// A running chain: the compiler folds it into v_max3_f32 with few NaN
+// canonicalizations of the MFMA results (a balanced tree needs one per leaf).
 __device__ __forceinline__ float tile_max(const f32x16_t (&s)[2]) {
   float mx = s[0][0];
 #pragma unroll
@@ -511,11 +513,16 @@ __device__ __forceinline__ void exp_tile(f32x16_t (&s)[2], float m_run, float c,
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int j = 0; j < 16; ++j) s[kb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c, -mc));
-  float psum[4] = {0.f, 0.f, 0.f, 0.f};
+  // four partial sums for ILP, each started from its first term (adding to
+  // +0 is not an identity the compiler may drop)
+  float psum[4];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) psum[2 * kb + (j >> 3)] += s[kb][j];
+    for (int j = 0; j < 16; ++j) {
+      float& acc = psum[2 * kb + (j >> 3)];
+      acc = (j & 7) == 0 ? s[kb][j] : acc + s[kb][j];
+    }
   l_run += (psum[0] + psum[1]) + (psum[2] + psum[3]);
 }
 
