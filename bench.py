@@ -21,8 +21,12 @@ prints one JSON line.
 * ``sweep``: the 2B generation sweep (32 layers x 13 scale steps, B=2,
   H=16, per-layer static keep policies at budget 0.1): every layer-step runs
   SegmentedLayerCache.step (dense-prefix attention, activation pack,
-  segmented attention, append), timed per image, plus a phase split from a
-  separately profiled image (the profiler synchronizes each phase).
+  segmented attention, append), timed per image, eagerly and as replays of
+  the whole image captured in one HIP graph; ``per_scale_step``: the
+  same work split at the scale boundaries of one more image (HIP events,
+  no synchronization inside): ms for all 32 layers, us per layer-step and
+  attention TFLOP/s per scale; plus a phase split from a separately
+  profiled image (the profiler synchronizes each phase).
 * ``budgets_8b_class``: the 8B-class final step (B=8, H=32) at keep budgets
   0.05 / 0.1 / 0.2 / 1.0 (1.0 = every prior token kept, the dense-equivalent
   case), ms per step and TFLOP/s.
@@ -172,19 +176,24 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
     inputs = [W.generation_inputs(batch=batch, heads=heads, sides=sides, seed=2000 + l, device=device)
               for l in range(layers)]
     scale = 1.0 / math.sqrt(128)
-    flops = 0
+    step_flops = [0] * len(sides)
     for keep in keeps:
         for t, side in enumerate(sides):
             n = side * side
             for h in range(heads):
                 r = sum(sides[s] ** 2 for s in W.retained_scales(keep, t, h))
-                flops += batch * 4 * n * (r + n) * 128
+                step_flops[t] += batch * 4 * n * (r + n) * 128
+    flops = sum(step_flops)
 
-    def image():
+    def image(marks=None):
         for t in range(len(sides)):
+            if marks is not None:
+                marks[t].record(torch.cuda.current_stream(device))
             for l in range(layers):
                 q, k, v = inputs[l][t]
                 caches[l].step(q, k, v, t, scale)
+        if marks is not None:
+            marks[-1].record(torch.cuda.current_stream(device))
 
     image()
     stream = torch.cuda.current_stream(device)
@@ -197,6 +206,30 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
     t1.record(stream)
     torch.cuda.synchronize(device)
     ms = t0.elapsed_time(t1) / images
+    # the same image captured in one HIP graph (all 416 layer-steps): replays
+    # without the host's per-call work
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        image()
+    graph.replay()
+    torch.cuda.synchronize(device)
+    t0.record(stream)
+    for _ in range(images):
+        graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize(device)
+    ms_graph = t0.elapsed_time(t1) / images
+    del graph
+    # one more image with an event at every scale boundary: per-step times
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(sides) + 1)]
+    image(marks)
+    torch.cuda.synchronize(device)
+    per_step = []
+    for t in range(len(sides)):
+        step_ms = marks[t].elapsed_time(marks[t + 1])
+        per_step.append({"scale": t, "side": sides[t], "ms_all_layers": round(step_ms, 4),
+                         "us_per_layer_step": round(step_ms / layers * 1e3, 2),
+                         "attention_tflops": round(step_flops[t] / (step_ms * 1e-3) / 1e12, 1)})
     prof.set_real_pruning_fast_phase_profile_enabled(True)
     try:
         image()
@@ -205,8 +238,9 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
         prof.set_real_pruning_fast_phase_profile_enabled(False)
     return dict(what=f"{layers} layers x {len(sides)} scale steps, B={batch}, H={heads}, budget 0.1, "
                      "static per-layer keep policies (seed 1000 + layer)",
-                ms_per_image=round(ms, 3), attention_flops=flops,
+                ms_per_image=round(ms, 3), ms_per_image_graph=round(ms_graph, 3), attention_flops=flops,
                 tflops=round(flops / (ms * 1e-3) / 1e12, 1),
+                per_scale_step=per_step,
                 phase_gpu_ms_profiled={k: round(v, 3) for k, v in snap["cuda_ms"].items()},
                 phase_calls=snap["calls"],
                 copy_bytes_per_image=int(snap["segmented_flat_stats"].get("static_copy_bytes", 0)))

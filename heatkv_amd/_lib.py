@@ -25,6 +25,11 @@ HKV_ERR_DEVICE = -4
 
 DTYPE_CODES = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
 
+# Leading bytes of the attention workspace that must be zero before a call
+# (the per-item counters; the partial records behind them are written before
+# they are read).
+WORKSPACE_COUNTER_BYTES = 64 * 1024
+
 _lock = threading.Lock()
 _lib = None
 _device_ok: dict[int, bool] = {}
@@ -123,23 +128,29 @@ def dtype_code(dtype: torch.dtype) -> int:
 _workspaces: dict = {}
 
 
-def attention_workspace(device: torch.device):
-    """Zero-initialised workspace tensor of ``hkv_segmented_attention`` for the
-    current stream of ``device`` (None when HKV_ATTN_SPLIT=0: no item is cut).
-    The kernels leave it zeroed, so it is allocated and cleared once."""
+def attention_workspace(device: torch.device, stream=None):
+    """Workspace tensor (counters zeroed) of ``hkv_segmented_attention`` for the
+    current stream of ``device`` (or ``stream``, that stream) -- None when
+    HKV_ATTN_SPLIT=0: no item is cut.  The kernels leave it zeroed, so it is
+    allocated and cleared once."""
     if os.environ.get("HKV_ATTN_SPLIT", "1") == "0":
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    if stream is None:
+        stream = torch.cuda.current_stream(idx)
+    key = (idx, stream.cuda_stream)
     capturing = torch.cuda.is_current_stream_capturing()
     ws = None if capturing else _workspaces.get(key)
     if ws is None:
         need = int(load().hkv_segmented_attention_workspace_bytes(idx))
         if need < 0:
             check(need)
-        # under HIP-graph capture: a buffer of the graph's own pool, zeroed by a
-        # fill kernel the graph replays (no memset node), not cached
-        ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
-        if not capturing:
+        if capturing:
+            # a buffer of the graph's own pool, not cached; only its counters
+            # are cleared, by a fill kernel the graph replays (no memset node)
+            ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+            ws[:WORKSPACE_COUNTER_BYTES].zero_()
+        else:
+            ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
             _workspaces[key] = ws
     return ws

@@ -253,7 +253,8 @@ def fused_real_pruning_flat_segmented_attention(
         if return_lse
         else None
     )
-    ws = _lib.attention_workspace(q.device)
+    stream = torch.cuda.current_stream(q.device)
+    ws = _lib.attention_workspace(q.device, stream)
     code = _lib.load().hkv_segmented_attention(
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
         segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
@@ -264,7 +265,7 @@ def fused_real_pruning_flat_segmented_attention(
         _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
         float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
-        _lib.stream_handle(q.device),
+        stream.cuda_stream,
     )
     _lib.check(code)
     if return_lse:

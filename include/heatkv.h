@@ -88,8 +88,9 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *              the same mathematical result and this kernel always evaluates
  *              exp2 with scale*log2(e) folded in.
  *   workspace, workspace_bytes : NULL / 0, or device memory of at least
- *              hkv_segmented_attention_workspace_bytes(device) bytes, zeroed
- *              once before its first use (the calls leave it zeroed again).
+ *              hkv_segmented_attention_workspace_bytes(device) bytes whose
+ *              first 64 KiB (per-item counters) are zero before its first
+ *              use (the calls leave them zero again; the rest is scratch).
  *              With it, for 16-bit inputs, a launch with fewer than two
  *              rounds of (batch, head, 128-query tile) items per resident
  *              workgroup slot (2 per CU) cuts some items into two halves of
