@@ -26,6 +26,7 @@ from .policy import (  # noqa: F401
 from .enable import (  # noqa: F401
     METHOD_NAME,
     canonical_method,
+    enable_real_pruning_scale_specific_fast,
     enable_real_pruning_scale_specific_fused_segmented,
 )
 from .phase_profile import (  # noqa: F401

@@ -105,3 +105,33 @@ def enable_real_pruning_scale_specific_fused_segmented(
                 layer._pre_heatkv_kv_caching = layer.kv_caching
             layer.kv_caching = types.MethodType(real_scale_fused_segmented_kv_caching, layer)
     return model
+
+
+def enable_real_pruning_scale_specific_fast(
+    model,
+    budget,
+    scale_specific_removal_orders,
+    *,
+    protected_prefix_scales: int = 4,
+    source_scale_start: Optional[int] = None,
+    skip_last_scale: bool = True,
+    merge_mode: str = "exact",
+    attention_impl: str = "fused_segmented",
+    requested_generation_batch_size: Optional[int] = None,
+    module_filter: Optional[Callable] = None,
+    sides: Sequence[int] = SIDES_1M,
+    patch_forward: bool = True,
+):
+    """The reference's general entry (enable_real_pruning_fast.py:2279-2378):
+    ``attention_impl`` must be ``"fused_segmented"`` (the only implementation
+    the reference has too); then as
+    :func:`enable_real_pruning_scale_specific_fused_segmented`."""
+    if merge_mode != "exact":
+        raise ValueError("real pruning fast v1 only supports merge_mode='exact'")
+    if attention_impl != "fused_segmented":
+        raise ValueError(f"unsupported real pruning fast attention_impl: {attention_impl!r}")
+    return enable_real_pruning_scale_specific_fused_segmented(
+        model, budget, scale_specific_removal_orders, protected_prefix_scales=protected_prefix_scales,
+        source_scale_start=source_scale_start, skip_last_scale=skip_last_scale, merge_mode=merge_mode,
+        requested_generation_batch_size=requested_generation_batch_size, module_filter=module_filter,
+        sides=sides, patch_forward=patch_forward)

@@ -203,3 +203,26 @@ def test_enable_attaches_policy_schedule_and_cache():
     assert canonical_method("fused-segmented") == canonical_method("fused_segmented") == "real_scale_fused_segmented"
     with pytest.raises(ValueError):
         canonical_method("dense")
+
+
+def test_general_enable_entry_checks_attention_impl():
+    import torch
+
+    from heatkv_amd import enable_real_pruning_scale_specific_fast
+
+    class SelfAttention(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.num_heads = H
+
+    model = torch.nn.Sequential(*[SelfAttention() for _ in range(L)])
+    with pytest.raises(ValueError, match="unsupported real pruning fast attention_impl: 'dense'"):
+        enable_real_pruning_scale_specific_fast(model, 0.1, ORDERS, attention_impl="dense")
+    with pytest.raises(ValueError, match="merge_mode='exact'"):
+        enable_real_pruning_scale_specific_fast(model, 0.1, ORDERS, merge_mode="approx")
+    out = enable_real_pruning_scale_specific_fast(model, 0.1, ORDERS, protected_prefix_scales=START,
+                                                  source_scale_start=START)
+    assert out is model and [m.layer_idx for m in model] == list(range(L))
+    want = GOLD["strict"]["0.1"]["removed_mask"]
+    ctrl = model[0].heatkv_controller
+    assert all(_mask(ctrl, t, s) == want[str(t)][str(s)] for t in range(13) for s in range(START, 12))
