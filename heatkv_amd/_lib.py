@@ -126,31 +126,74 @@ def dtype_code(dtype: torch.dtype) -> int:
 # Attention workspaces, one per (device, stream): calls on one stream run in
 # order, so they can share one; calls on different streams may overlap.
 _workspaces: dict = {}
+# Under HIP-graph capture: one per (device, stream) and capture, from the
+# graph's own pool: (capture id, tensor).
+_capture_workspaces: dict = {}
+_hip_rt = None
+
+
+def _hip_runtime():
+    """The HIP runtime library torch loaded (for stream-capture queries)."""
+    global _hip_rt
+    if _hip_rt is None:
+        path = "libamdhip64.so"
+        try:
+            with open("/proc/self/maps") as fh:
+                for line in fh:
+                    if "libamdhip64" in line:
+                        path = line.split()[-1]
+                        break
+        except OSError:
+            pass
+        lib = ctypes.CDLL(path)
+        fn = lib.hipStreamGetCaptureInfo
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_ulonglong)]
+        _hip_rt = lib
+    return _hip_rt
+
+
+def capture_id(stream_handle: int) -> int:
+    """Id of the graph capture running on the stream (0 when none)."""
+    status = ctypes.c_int(0)
+    cid = ctypes.c_ulonglong(0)
+    err = _hip_runtime().hipStreamGetCaptureInfo(ctypes.c_void_p(stream_handle), ctypes.byref(status),
+                                                 ctypes.byref(cid))
+    if err != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed with HIP error {err}")
+    return int(cid.value) if status.value == 1 else 0  # 1 = hipStreamCaptureStatusActive
 
 
 def attention_workspace(device: torch.device, stream=None):
     """Workspace tensor (counters zeroed) of ``hkv_segmented_attention`` for the
     current stream of ``device`` (or ``stream``, that stream) -- None when
-    HKV_ATTN_SPLIT=0: no item is cut.  The kernels leave it zeroed, so it is
-    allocated and cleared once."""
+    HKV_ATTN_SPLIT=0: no item is cut.  The kernels leave the counters zeroed,
+    so a stream's workspace is allocated and cleared once; under HIP-graph
+    capture, once per capture (from the graph's pool, cleared by a fill kernel
+    that the graph replays before the first call, no memset node)."""
     if os.environ.get("HKV_ATTN_SPLIT", "1") == "0":
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if stream is None:
         stream = torch.cuda.current_stream(idx)
     key = (idx, stream.cuda_stream)
-    capturing = torch.cuda.is_current_stream_capturing()
-    ws = None if capturing else _workspaces.get(key)
+    if torch.cuda.is_current_stream_capturing():
+        cid = capture_id(stream.cuda_stream)
+        hit = _capture_workspaces.get(key)
+        if hit is not None and hit[0] == cid:
+            return hit[1]
+        need = int(load().hkv_segmented_attention_workspace_bytes(idx))
+        if need < 0:
+            check(need)
+        ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+        ws[:WORKSPACE_COUNTER_BYTES].zero_()
+        _capture_workspaces[key] = (cid, ws)  # an earlier capture's buffer stays with its graph
+        return ws
+    ws = _workspaces.get(key)
     if ws is None:
         need = int(load().hkv_segmented_attention_workspace_bytes(idx))
         if need < 0:
             check(need)
-        if capturing:
-            # a buffer of the graph's own pool, not cached; only its counters
-            # are cleared, by a fill kernel the graph replays (no memset node)
-            ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", idx))
-            ws[:WORKSPACE_COUNTER_BYTES].zero_()
-        else:
-            ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
-            _workspaces[key] = ws
+        ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _workspaces[key] = ws
     return ws

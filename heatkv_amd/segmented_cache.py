@@ -162,11 +162,20 @@ class SegmentedLayerCache:
             self._tables_by_len[key] = hit
         return hit
 
+    def _empty_tables(self, heads: int, device):
+        """Tables with no segment (attention over the current scale only), made once."""
+        key = ("empty", heads, str(device))
+        hit = self._tables_by_len.get(key)
+        if hit is None:
+            empty = torch.zeros((heads, 0), dtype=torch.int32, device=device)
+            hit = (empty, empty, torch.zeros((heads,), dtype=torch.int32, device=device))
+            self._tables_by_len[key] = hit
+        return hit
+
     def _attend_dense(self, q, k, v, scale, mode):
         B, H, L, D = q.shape
         if self.cached_k is None or self.logical_len == 0:
-            empty = torch.zeros((H, 0), dtype=torch.int32, device=q.device)
-            tables = (empty, empty, torch.zeros((H,), dtype=torch.int32, device=q.device))
+            tables = self._empty_tables(H, q.device)
             slab_k = slab_v = None
         else:
             T = self.cached_k.shape[2]

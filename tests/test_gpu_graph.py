@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from heatkv_amd import _lib
 from heatkv_amd import harness as Hn
 from heatkv_amd.slab_schedule import SIDES_1M
 from heatkv_amd.workloads import generation_inputs
@@ -40,8 +41,12 @@ def test_graph_replays_match_eager(device, method):
     torch.cuda.synchronize(device)
     want = [bits(o) for o in sink]
     g = torch.cuda.CUDAGraph()
+    before = dict(_lib._capture_workspaces)
     with torch.cuda.graph(g):
         generation()
+    # one workspace for the whole capture (the calls run in order on its stream)
+    new = [v for k, v in _lib._capture_workspaces.items() if before.get(k) is not v]
+    assert len(new) == 1 and new[0][0] != 0
     outs = list(sink)
     for rep in range(3):
         print(f"[graph] {method}: replay {rep}", flush=True)
