@@ -17,8 +17,6 @@ unchanged.
 
 from __future__ import annotations
 
-import numpy as np
-
 
 def pack_flat_segments(dst, src, dst_starts, src_starts, lengths):
     """In-place copy into ``dst`` ``[B, C, D]`` from ``src`` ``[B, S, D]``; returns ``dst``."""
