@@ -171,6 +171,34 @@ __device__ __forceinline__ void compute_head_rows(const int32_t* __restrict__ se
   }
 }
 
+// Exclusive prefix of segment lengths in place, by one wave: on entry
+// seg_pref[i + 1] holds the length of entry i < nseg (nseg <= 256), on exit
+// seg_pref[i] = sum of the lengths before entry i (seg_pref[nseg] = total).
+__device__ __forceinline__ void length_prefix(int32_t* seg_pref, int nseg, int lane) {
+  int v[4];
+  int local = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = lane * 4 + k;
+    v[k] = idx < nseg ? seg_pref[idx + 1] : 0;
+    local += v[k];
+  }
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  int run = incl - local;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = lane * 4 + k;
+    run += v[k];
+    if (idx < nseg) seg_pref[idx + 1] = run;
+  }
+  if (lane == 0) seg_pref[0] = 0;
+}
+
 // Head h's clamped segment starts and exclusive length prefix into LDS (ends
 // with a workgroup barrier); returns the live entry count, w.R = its total.
 template <int kThreads>
@@ -193,30 +221,7 @@ __device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ s
     seg_pref[i + 1] = en > st ? static_cast<int32_t>(en - st) : 0;
   }
   __syncthreads();
-  if (wave == 0) {
-    int v[4];
-    int local = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int idx = lane * 4 + k;
-      v[k] = idx < nseg ? seg_pref[idx + 1] : 0;
-      local += v[k];
-    }
-    int incl = local;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    int run = incl - local;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int idx = lane * 4 + k;
-      run += v[k];
-      if (idx < nseg) seg_pref[idx + 1] = run;
-    }
-    if (lane == 0) seg_pref[0] = 0;
-  }
+  if (wave == 0) length_prefix(seg_pref, nseg, lane);
   __syncthreads();
   w.nseg = nseg;
   w.R = seg_pref[nseg];
@@ -296,30 +301,7 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
     seg_pref[i + 1] = tab_len[w.h * S + i];
   }
   __syncthreads();
-  if (tid < 64) {
-    int v[4];
-    int local = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int idx = lane * 4 + k;
-      v[k] = idx < nseg ? seg_pref[idx + 1] : 0;
-      local += v[k];
-    }
-    int incl = local;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    int run = incl - local;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int idx = lane * 4 + k;
-      run += v[k];
-      if (idx < nseg) seg_pref[idx + 1] = run;
-    }
-    if (lane == 0) seg_pref[0] = 0;
-  }
+  if (tid < 64) length_prefix(seg_pref, nseg, lane);
   __syncthreads();
   w.nseg = nseg;
   w.R = seg_pref[nseg];
