@@ -46,6 +46,41 @@ from .real_pruning_fused_attention import _fused_qk_dot_mode_id
 _QK_DOT_TF32 = 1
 
 
+def _versions(*tensors):
+    return tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
+
+
+def _autocast_dtype(x):
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return None
+
+
+def _qkv_bias(layer, x):
+    """``cat(q_bias, zero_k_bias, v_bias)`` as the projection takes it (cast to
+    the autocast dtype, as autocast casts it), remade only when a bias tensor
+    changes (its storage or version): parameters do not change between the
+    steps of a generation, and each remake costs the chain two small kernels."""
+    dtype = _autocast_dtype(x)
+    key = (_versions(layer.q_bias, layer.zero_k_bias, layer.v_bias), dtype)
+    hit = getattr(layer, "_heatkv_qkv_bias", None)
+    if hit is None or hit[0] != key:
+        bias = torch.cat((layer.q_bias, layer.zero_k_bias, layer.v_bias))
+        hit = (key, bias if dtype is None else bias.to(dtype))
+        layer._heatkv_qkv_bias = hit
+    return hit[1]
+
+
+def _scale_mul(layer):
+    """:func:`scale_mul_of` of the layer, remade only when ``scale_mul_1H11`` changes."""
+    key = (_versions(layer.scale_mul_1H11), float(layer.max_scale_mul))
+    hit = getattr(layer, "_heatkv_scale_mul", None)
+    if hit is None or hit[0] != key:
+        hit = (key, scale_mul_of(layer))
+        layer._heatkv_scale_mul = hit
+    return hit[1]
+
+
 def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, attn_fn=None,
                                        scale_schedule=None, rope2d_freqs_grid=None, scale_ind=0):
     if not self.caching:
@@ -56,8 +91,7 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
         raise NotImplementedError("real pruning fused segmented does not support custom attention functions")
 
     batch_size, seq_len, _ = x.shape
-    qkv = F.linear(input=x, weight=self.mat_qkv.weight,
-                   bias=torch.cat((self.q_bias, self.zero_k_bias, self.v_bias)))
+    qkv = F.linear(input=x, weight=self.mat_qkv.weight, bias=_qkv_bias(self, x))
     table = None
     start = 0
     if rope2d_freqs_grid is not None:
@@ -76,7 +110,7 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
     append = cache.producer_append(int(scale_ind), qk_dtype, qkv.device)
     q, k, v = qkv_produce(
         qkv.view(batch_size, seq_len, 3 * self.num_heads * self.head_dim), self.num_heads,
-        scale_mul=scale_mul_of(self) if cos_attn else None, rope_table=table, rope_start_row=start,
+        scale_mul=_scale_mul(self) if cos_attn else None, rope_table=table, rope_start_row=start,
         normalize=cos_attn, qk_dtype=qk_dtype, append=append)
     del qkv
     output = cache.step(q, k, v, int(scale_ind), float(self.scale), appended=append is not None)

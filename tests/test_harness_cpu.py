@@ -51,3 +51,22 @@ def test_synthetic_layers_get_the_patched_forward():
                          initial_scales=3, orders=orders)
     ctrl = base[0].heatkv_controller
     assert all(not any(ctrl.removed_heads_by_source_for(l, t).values()) for l in range(2) for t in range(13))
+
+
+def test_forward_parameter_caches_follow_parameter_updates():
+    from heatkv_amd import attention_forward as AF
+
+    layer = Hn.SyntheticSelfAttention(256, 2, seed=3)
+    x = torch.zeros((1, 4, 256))
+    b1 = AF._qkv_bias(layer, x)
+    assert AF._qkv_bias(layer, x) is b1
+    assert torch.equal(b1, torch.cat((layer.q_bias, layer.zero_k_bias, layer.v_bias)))
+    s1 = AF._scale_mul(layer)
+    assert AF._scale_mul(layer) is s1
+    with torch.no_grad():
+        layer.q_bias.add_(1.0)
+        layer.scale_mul_1H11.fill_(10.0)  # clamped at log(100)
+    b2 = AF._qkv_bias(layer, x)
+    assert b2 is not b1 and torch.equal(b2, torch.cat((layer.q_bias, layer.zero_k_bias, layer.v_bias)))
+    s2 = AF._scale_mul(layer)
+    assert s2 is not s1 and torch.allclose(s2, torch.full((2,), 100.0))
