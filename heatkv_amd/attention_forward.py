@@ -113,7 +113,10 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
         scale_mul=_scale_mul(self) if cos_attn else None, rope_table=table, rope_start_row=start,
         normalize=cos_attn, qk_dtype=qk_dtype, append=append)
     del qkv
-    output = cache.step(q, k, v, int(scale_ind), float(self.scale), appended=append is not None)
+    # under autocast the projection takes the attention output in the autocast
+    # dtype: the kernel writes it rounded once, as autocast's cast would
+    output = cache.step(q, k, v, int(scale_ind), float(self.scale), appended=append is not None,
+                        out_dtype=_autocast_dtype(x))
     return self.proj_drop(self.proj(output))
 
 

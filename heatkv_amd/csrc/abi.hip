@@ -110,7 +110,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 void* out, float* lse, int32_t batch, int32_t heads,
                                 int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
                                 int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
-                                int32_t v_dtype, float softmax_scale, int32_t use_exp2,
+                                int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (head_dim != 128)
@@ -126,6 +126,10 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                 "real_scale_fused_segmented supports only float16, bfloat16, or float32 tensors");
   if (q_dtype != k_dtype)
     return fail(HKV_ERR_UNSUPPORTED, "q and k must share one dtype (got %d and %d)", q_dtype, k_dtype);
+  if (out_dtype == 0) out_dtype = q_dtype;
+  if (elem_bytes(out_dtype) == 0)
+    return fail(HKV_ERR_UNSUPPORTED, "out_dtype must be 0 (q's dtype), float16, bfloat16 or float32 (got %d)",
+                out_dtype);
   if (max_segments < 0 || max_segments > hkv::kMaxSegments)
     return fail(HKV_ERR_UNSUPPORTED, "max_segments must be in [0, %d] (got %d)", hkv::kMaxSegments,
                 max_segments);
@@ -176,6 +180,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   a.q_dtype = q_dtype;
   a.k_dtype = k_dtype;
   a.v_dtype = v_dtype;
+  a.out_dtype = out_dtype;
   a.workspace = workspace;
   a.workspace_bytes = workspace != nullptr ? workspace_bytes : 0;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));

@@ -529,16 +529,12 @@ __device__ __forceinline__ u32x4_t p_operand(const f32x16_t (&s)[2], int u) {
   return pf;
 }
 
-// O = acc / l to out[b, q, h*D + d] (d = 32db + 8(j>>2) + 4g + (j&3)), and
+// O = acc / l to out[b, q, h*D + d] (d = 32db + 8(j>>2) + 4g + (j&3)) in
+// `out_dtype` (fp32, or rounded to nearest even to bf16 / fp16), and
 // lse = ln(2) (c m + log2(l)) for the lane's query (c = scale log2(e)).
-template <int QDT>
-__device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_run, float l_run,
-                                             float c, void* out, float* lse, int64_t b, int64_t h,
-                                             int32_t qrow, int L, int H, int64_t bh, int g) {
-  const float l_tot = pair_sum(l_run);
-  const float inv = 1.f / l_tot;
-  if (qrow >= L) return;
-  const int64_t out_row = (b * L + qrow) * (static_cast<int64_t>(H) * kD) + h * kD;
+template <int DT>
+__device__ __forceinline__ void store_rows(const f32x16_t (&oacc)[4], float inv, void* out, int64_t out_row,
+                                           int g) {
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -548,8 +544,21 @@ __device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_
       v[1] = oacc[db][4 * jb + 1] * inv;
       v[2] = oacc[db][4 * jb + 2] * inv;
       v[3] = oacc[db][4 * jb + 3] * inv;
-      store4<QDT>(out, out_row + db * 32 + 8 * jb + 4 * g, v);
+      store4<DT>(out, out_row + db * 32 + 8 * jb + 4 * g, v);
     }
+}
+
+__device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_run, float l_run,
+                                             float c, void* out, float* lse, int64_t b, int64_t h,
+                                             int32_t qrow, int L, int H, int64_t bh, int g,
+                                             int32_t out_dtype) {
+  const float l_tot = pair_sum(l_run);
+  const float inv = 1.f / l_tot;
+  if (qrow >= L) return;
+  const int64_t out_row = (b * L + qrow) * (static_cast<int64_t>(H) * kD) + h * kD;
+  if (out_dtype == kF32) store_rows<kF32>(oacc, inv, out, out_row, g);
+  else if (out_dtype == kF16) store_rows<kF16>(oacc, inv, out, out_row, g);
+  else store_rows<kBF16>(oacc, inv, out, out_row, g);
   if (lse != nullptr && g == 0) lse[bh * L + qrow] = (m_run * c + __log2f(l_tot)) * 0.6931471805599453f;
 }
 

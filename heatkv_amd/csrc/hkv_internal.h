@@ -51,6 +51,7 @@ struct AttnArgs {
   int32_t q_dtype;
   int32_t k_dtype;
   int32_t v_dtype;
+  int32_t out_dtype;        // element type of `out` (q_dtype by default)
   void* workspace;          // round-split storage, or null
   int64_t workspace_bytes;
 };

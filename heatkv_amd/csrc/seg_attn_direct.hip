@@ -156,7 +156,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
     }
     l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
   }
-  write_output<QDT>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  write_output(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
   if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   }
 
   if (parts == 1) {
-    write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+    write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
     return;
   }
   merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);

@@ -226,7 +226,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
     }
     __syncthreads();
   }
-  write_output<QDT>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g);
+  write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
 }
 
 template <int QDT, int KDT, int VDT>

@@ -161,13 +161,15 @@ def fused_real_pruning_flat_segmented_attention(
     allow_cpu_fallback: bool = False,
     softmax_mode: str = "exp",
     return_lse: bool = False,
+    out_dtype: Optional[torch.dtype] = None,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
 
     ``persisted_k/v`` are ``[B, capacity, D]``; ``segment_starts/ends [H, S]``
     are row offsets into that slab grouped per head, ``segment_counts [H]``.
-    Returns ``[B, L, H*D]`` in q's dtype (and ``lse [B, H, L]`` fp32 when
-    ``return_lse``).  Mirrors fused_real_pruning_flat_segmented_attention
+    Returns ``[B, L, H*D]`` in q's dtype, or ``out_dtype`` (an extension: the
+    fp32 result rounded once to bf16 / fp16, what casting q's-dtype output
+    would give), and ``lse [B, H, L]`` fp32 when ``return_lse``.  Mirrors fused_real_pruning_flat_segmented_attention
     (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
     ``hkv_segmented_attention``.
     """
@@ -229,6 +231,10 @@ def fused_real_pruning_flat_segmented_attention(
             )
     if q.dtype != current_k.dtype:
         raise RuntimeError("real_scale_fused_segmented requires q and k of one dtype")
+    if out_dtype is None:
+        out_dtype = q.dtype
+    if out_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("out_dtype must be torch.float16, torch.bfloat16 or torch.float32")
 
     # Knobs are validated like the reference's (bad values raise ValueError).
     for knob, default in (("REAL_PRUNING_FUSED_BLOCK_M", 64), ("REAL_PRUNING_FUSED_BLOCK_N", 64),
@@ -247,7 +253,7 @@ def fused_real_pruning_flat_segmented_attention(
     current_k = current_k.contiguous()
     current_v = current_v.contiguous()
 
-    output = q.new_empty((batch_size, current_len, num_heads * head_dim))
+    output = torch.empty((batch_size, current_len, num_heads * head_dim), device=q.device, dtype=out_dtype)
     lse = (
         torch.empty((batch_size, num_heads, current_len), device=q.device, dtype=torch.float32)
         if return_lse
@@ -263,7 +269,7 @@ def fused_real_pruning_flat_segmented_attention(
         batch_size, num_heads, current_len,
         int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
         _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
-        float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
+        _lib.dtype_code(out_dtype), float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         stream.cuda_stream,
     )

@@ -172,7 +172,7 @@ class SegmentedLayerCache:
             self._tables_by_len[key] = hit
         return hit
 
-    def _attend_dense(self, q, k, v, scale, mode):
+    def _attend_dense(self, q, k, v, scale, mode, out_dtype=None):
         B, H, L, D = q.shape
         if self.cached_k is None or self.logical_len == 0:
             tables = self._empty_tables(H, q.device)
@@ -185,7 +185,7 @@ class SegmentedLayerCache:
         return fused_real_pruning_flat_segmented_attention(
             q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=tables[0],
             segment_ends=tables[1], segment_counts=tables[2], current_k=k, current_v=v,
-            softmax_scale=scale, softmax_mode=mode)
+            softmax_scale=scale, softmax_mode=mode, out_dtype=out_dtype)
 
     # ------------------------------------------------------------------ step
 
@@ -205,11 +205,13 @@ class SegmentedLayerCache:
         return self.cached_k, self.cached_v, offsets
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale_ind: int,
-             softmax_scale: float, softmax_mode: Optional[str] = None, appended: bool = False) -> torch.Tensor:
+             softmax_scale: float, softmax_mode: Optional[str] = None, appended: bool = False,
+             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
         """Attention of scale ``scale_ind`` and the cache update for the next scale.
 
         ``appended``: the producer already wrote the rows offered by
-        :meth:`producer_append` for this scale; only the other heads are copied."""
+        :meth:`producer_append` for this scale; only the other heads are copied.
+        ``out_dtype``: element type of the output (q's by default)."""
         if appended and not self.active:
             raise RuntimeError("appended=True needs an active slab (see producer_append)")
         mode = fused_softmax_mode() if softmax_mode is None else softmax_mode
@@ -220,7 +222,7 @@ class SegmentedLayerCache:
         if baseline_prefix_enabled() and not self.active and not has_removed(self.removed(scale_ind)):
             # dense prefix (:1972-2038)
             with prof.phase("attention"):
-                out = self._attend_dense(q, k, v, softmax_scale, mode)
+                out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
             if final:
                 self.reset()
                 return out
@@ -242,10 +244,10 @@ class SegmentedLayerCache:
         dense_candidate = None
         if old_len == 0:
             with prof.phase("attention"):
-                out = self._attend_dense(q, k, v, softmax_scale, mode)
+                out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
         elif not self.active and not has_removed(self.removed(scale_ind)):
             with prof.phase("attention"):
-                out = self._attend_dense(q, k, v, softmax_scale, mode)
+                out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
             with prof.phase("materialize"):
                 dense_candidate = (torch.cat((self.cached_k, k), dim=2), torch.cat((self.cached_v, v), dim=2))
                 prof.stat_add("dense_attention_cat_calls")
@@ -258,7 +260,8 @@ class SegmentedLayerCache:
                 out = fused_real_pruning_flat_segmented_attention(
                     q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
                     segment_starts=starts, segment_ends=ends, segment_counts=counts,
-                    current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode)
+                    current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
+                    out_dtype=out_dtype)
 
         with prof.phase("compact"):
             if final:

@@ -80,7 +80,9 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *   q, cur_k, cur_v : [batch, heads, cur_len, head_dim] contiguous
  *   slab_k, slab_v  : [batch, slab_capacity, head_dim] contiguous
  *   seg_starts, seg_ends : int32 [heads, max_segments]; seg_counts : int32 [heads]
- *   out  : [batch, cur_len, heads*head_dim], element type q_dtype
+ *   out  : [batch, cur_len, heads*head_dim] of out_dtype (0 = q_dtype, as in
+ *          the reference; bf16 / fp16 store the fp32 result rounded to
+ *          nearest even, what a later cast of an fp32 output would give)
  *   lse  : NULL, or float32 [batch, heads, cur_len] natural-log log-sum-exp
  *          of the scaled scores (not produced by the reference kernel)
  *   *_dtype : HKV_DTYPE_*; slab and current K share k_dtype, V share v_dtype
@@ -110,7 +112,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t batch, int32_t heads, int32_t cur_len,
                                 int64_t slab_capacity, int32_t max_segments, int32_t head_dim,
                                 int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
-                                float softmax_scale, int32_t use_exp2,
+                                int32_t out_dtype, float softmax_scale, int32_t use_exp2,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

@@ -297,3 +297,23 @@ def test_attention_config4_budget_005(device):
     heads = sorted({order[0], order[-1]})
     print(f"[attn] config 4 budget 0.05 heads {heads} R={[r[h] for h in heads]}", flush=True)
     _check_workload(wl, device, heads=heads, batches=[2])
+
+
+@pytest.mark.parametrize("qk,out", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                    (torch.float32, torch.float16), (torch.bfloat16, torch.bfloat16)])
+def test_attention_out_dtype_is_a_single_rounding(qk, out, device):
+    """out_dtype writes the kernel's fp32 result rounded once: bit-identical to
+    the output in fp32 cast afterwards (both the 16-bit and the staged kernel)."""
+    wl = W.config(1)
+    slab_k, slab_v = W.build_slab(wl, device)
+    st, en, ct = wl.schedule.device_tables(wl.target, device)
+    kw = dict(q=wl.q.to(device, qk), persisted_k=slab_k.to(qk), persisted_v=slab_v, segment_starts=st,
+              segment_ends=en, segment_counts=ct, current_k=wl.cur_k.to(device, qk),
+              current_v=wl.cur_v.to(device), softmax_scale=wl.softmax_scale)
+    got = fused_real_pruning_flat_segmented_attention(**kw, out_dtype=out)
+    full = fused_real_pruning_flat_segmented_attention(**kw, out_dtype=torch.float32)
+    torch.cuda.synchronize(device)
+    assert got.dtype == out and full.dtype == torch.float32
+    assert torch.equal(got, full.to(out))
+    with pytest.raises(ValueError, match="out_dtype"):
+        fused_real_pruning_flat_segmented_attention(**kw, out_dtype=torch.int32)
