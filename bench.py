@@ -17,16 +17,25 @@ prints one JSON line.
   ``traffic`` is the HBM bytes per launch from the committed rocprofv3
   FETCH_SIZE / WRITE_SIZE summary in profiles/ (copy-calibrated).
 * ``compaction``: the slab fill (one append launch per kept prior scale)
-  against HBM bandwidth, timed separately.
+  against HBM bandwidth, issued eagerly and as graph replays (device time);
+  these launches move 0.02-2 MB each and are latency-bound.
+  ``compaction_8b_dense`` (with the budget leg): the same fill for the
+  8B-class workload at budget 1.0 (12 launches, 1.7 GB), where the pack
+  kernel meets the HBM bound.
 * ``sweep``: the 2B generation sweep (32 layers x 13 scale steps, B=2,
   H=16, per-layer static keep policies at budget 0.1): every layer-step runs
   SegmentedLayerCache.step (dense-prefix attention, activation pack,
   segmented attention, append), timed per image, eagerly and as replays of
-  the whole image captured in one HIP graph; ``per_scale_step``: the
-  same work split at the scale boundaries of one more image (HIP events,
-  no synchronization inside): ms for all 32 layers, us per layer-step and
-  attention TFLOP/s per scale; plus a phase split from a separately
-  profiled image (the profiler synchronizes each phase).
+  the whole image captured in one HIP graph; ``per_scale_step``: the image
+  captured as one graph per scale (all layers), replayed in order with HIP
+  events between the replays: ms for all 32 layers, us per layer-step,
+  attention TFLOP/s and the fraction of the step's roofline (max of its
+  attention FLOPs at the bf16 peak and its algorithmic HBM bytes at 8 TB/s;
+  bytes = q, current K/V, output, retained prior K/V and every copied row
+  read + written once); ``graph_kernel_floor_us``: device time per kernel
+  node of a replayed graph of one-element kernels, the latency floor of the
+  small scales; plus a phase split from a separately profiled image (the
+  profiler synchronizes each phase).
 * ``budgets_8b_class``: the 8B-class final step (B=8, H=32) at keep budgets
   0.05 / 0.1 / 0.2 / 1.0 (1.0 = every prior token kept, the dense-equivalent
   case), ms per step and TFLOP/s.
@@ -123,7 +132,11 @@ def time_attention(kw, device, steps, warmup):
 
 
 def time_pack(wl, device, reps=20):
-    """Average duration of the slab fill (all prior appends) and its algorithmic bytes."""
+    """The slab fill of ``wl`` (one append launch per kept prior scale):
+    average duration issued eagerly (host work per launch included) and as
+    replays of the launches captured in one HIP graph (device time only),
+    algorithmic bytes (read + write of every packed row), launch count and
+    the bytes of the largest launch."""
     import torch
 
     from heatkv_amd import pack_flat_segments_kv
@@ -134,6 +147,7 @@ def time_pack(wl, device, reps=20):
     slab_v = torch.empty_like(slab_k)
     calls = []
     nbytes = 0
+    largest = 0
     esz = wl.prior_k.element_size() + wl.prior_v.element_size()
     for s, plan in wl.prior_append_plans():
         a, b = sched.scale_ranges[s]
@@ -143,20 +157,25 @@ def time_pack(wl, device, reps=20):
         calls.append(dict(dst_k=slab_k, dst_v=slab_v, src_k=sk, src_v=sv, dst_starts=meta[0],
                           src_starts=meta[1], lengths=meta[2], max_length=plan.max_length))
         nbytes += B * plan.slots * D * esz * 2
-    for c in calls:
-        pack_flat_segments_kv(**c)
-    stream = torch.cuda.current_stream(device)
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(device)
-    t0.record(stream)
-    for _ in range(reps):
+        largest = max(largest, B * plan.slots * D * esz * 2)
+
+    def fill():
         for c in calls:
             pack_flat_segments_kv(**c)
-    t1.record(stream)
-    torch.cuda.synchronize(device)
-    ms = t0.elapsed_time(t1) / reps
-    return ms, nbytes, len(calls)
+
+    ms = _events_ms(fill, device, reps, 3)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fill()
+    ms_graph = _events_ms(graph.replay, device, reps, 3)
+    launches = len(calls)
+    del graph, calls, slab_k, slab_v
+    torch.cuda.empty_cache()
+    return {"ms": round(ms, 5), "ms_graph": round(ms_graph, 5), "bytes": nbytes, "launches": launches,
+            "largest_launch_bytes": largest,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "GB/s_graph": round(nbytes / (ms_graph * 1e-3) / 1e9, 1),
+            "frac_hbm_graph": round(nbytes / (ms_graph * 1e-3) / PEAK_HBM_BPS, 4)}
 
 
 def time_sweep(device, images, layers=32, heads=16, batch=2):
@@ -184,6 +203,22 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
                 r = sum(sides[s] ** 2 for s in W.retained_scales(keep, t, h))
                 step_flops[t] += batch * 4 * n * (r + n) * 128
     flops = sum(step_flops)
+    # algorithmic HBM bytes per scale step: q, current K/V and the output
+    # (bf16), every retained prior row of K/V read once, and each copied row
+    # (append / activation pack) read and written once
+    step_bytes = [0] * len(sides)
+    for keep, cache in zip(keeps, caches):
+        for t, side in enumerate(sides):
+            n = side * side
+            r = sum(sides[s] ** 2 for h in range(heads) for s in W.retained_scales(keep, t, h))
+            copied = 0
+            plan = cache.schedule.append_plans.get((t, t + 1))
+            if plan is not None:
+                copied += plan.slots
+            act = cache.schedule.activation_plans.get(t + 1)  # packed at the end of step t
+            if act is not None:
+                copied += act.slots
+            step_bytes[t] += batch * 128 * 2 * (4 * heads * n + 2 * r + 4 * copied)
 
     def image(marks=None):
         for t in range(len(sides)):
@@ -220,16 +255,45 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
     torch.cuda.synchronize(device)
     ms_graph = t0.elapsed_time(t1) / images
     del graph
-    # one more image with an event at every scale boundary: per-step times
+    # per-scale graphs: the image captured as 13 graphs (one per scale, all
+    # layers; one shared memory pool, replayed in capture order), with events
+    # between the replays: device time of each scale step without host work
+    pool = None
+    scale_graphs = []
+    for t in range(len(sides)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            for l in range(layers):
+                q, k, v = inputs[l][t]
+                caches[l].step(q, k, v, t, scale)
+        pool = g.pool()
+        scale_graphs.append(g)
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(sides) + 1)]
-    image(marks)
+    step_ms = [0.0] * len(sides)
+    reps = max(1, images)
+    for g in scale_graphs:
+        g.replay()
     torch.cuda.synchronize(device)
+    for _ in range(reps):
+        marks[0].record(stream)
+        for t, g in enumerate(scale_graphs):
+            g.replay()
+            marks[t + 1].record(stream)
+        torch.cuda.synchronize(device)
+        for t in range(len(sides)):
+            step_ms[t] += marks[t].elapsed_time(marks[t + 1]) / reps
+    del scale_graphs
+    floor_us = graph_launch_floor_us(device)
     per_step = []
     for t in range(len(sides)):
-        step_ms = marks[t].elapsed_time(marks[t + 1])
-        per_step.append({"scale": t, "side": sides[t], "ms_all_layers": round(step_ms, 4),
-                         "us_per_layer_step": round(step_ms / layers * 1e3, 2),
-                         "attention_tflops": round(step_flops[t] / (step_ms * 1e-3) / 1e12, 1)})
+        roof_ms = max(step_flops[t] / PEAK_BF16_FLOPS, step_bytes[t] / PEAK_HBM_BPS) * 1e3
+        per_step.append({"scale": t, "side": sides[t], "ms_all_layers": round(step_ms[t], 4),
+                         "us_per_layer_step": round(step_ms[t] / layers * 1e3, 2),
+                         "attention_tflops": round(step_flops[t] / (step_ms[t] * 1e-3) / 1e12, 1),
+                         "roofline_us_per_layer_step": round(roof_ms / layers * 1e3, 3),
+                         "roofline_bound": "mfma" if step_flops[t] / PEAK_BF16_FLOPS
+                         >= step_bytes[t] / PEAK_HBM_BPS else "hbm",
+                         "frac_roofline": round(roof_ms / step_ms[t], 4)})
     prof.set_real_pruning_fast_phase_profile_enabled(True)
     try:
         image()
@@ -240,7 +304,7 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
                      "static per-layer keep policies (seed 1000 + layer)",
                 ms_per_image=round(ms, 3), ms_per_image_graph=round(ms_graph, 3), attention_flops=flops,
                 tflops=round(flops / (ms * 1e-3) / 1e12, 1),
-                per_scale_step=per_step,
+                per_scale_step=per_step, graph_kernel_floor_us=round(floor_us, 2),
                 phase_gpu_ms_profiled={k: round(v, 3) for k, v in snap["cuda_ms"].items()},
                 phase_calls=snap["calls"],
                 copy_bytes_per_image=int(snap["segmented_flat_stats"].get("static_copy_bytes", 0)))
@@ -342,6 +406,20 @@ def _events_ms(fn, device, reps, warmup):
     t1.record(stream)
     torch.cuda.synchronize(device)
     return t0.elapsed_time(t1) / reps
+
+
+def graph_launch_floor_us(device, nodes=64):
+    """Device time per kernel node of a replayed HIP graph of ``nodes`` one-element kernels."""
+    import torch
+
+    x = torch.zeros(1, device=device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(nodes):
+            x.add_(1.0)
+    ms = _events_ms(graph.replay, device, 20, 3)
+    del graph
+    return ms * 1e3 / nodes
 
 
 def measured_peaks(device):
@@ -486,7 +564,7 @@ def main():
     kw = attention_call(wl, device)
     ms_step, host_us = time_attention(kw, device, args.steps, args.warmup)
     achieved = flops / (ms_step * 1e-3)
-    pack_ms, pack_bytes, pack_calls = time_pack(wl, device)
+    pack = time_pack(wl, device)
     if args.copy_calib_mib > 0:
         copy_calibration(device, args.copy_calib_mib)
     rec = {
@@ -516,12 +594,8 @@ def main():
             "kernel": ATTN_KERNEL, "kernel_ms_mean": round(ms_step, 5),
         },
         "host_us_per_call": round(host_us, 1),
-        "compaction": {
-            "what": f"slab fill: {pack_calls} append launches (every kept prior scale)",
-            "ms": round(pack_ms, 5), "bytes": pack_bytes,
-            "GB/s": round(pack_bytes / (pack_ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(pack_bytes / (pack_ms * 1e-3) / PEAK_HBM_BPS, 4),
-        },
+        "compaction": dict(what=f"slab fill of {wl.name}: one append launch per kept prior scale",
+                           **pack),
     }
     if not args.no_producer:
         rec["producer"] = time_producer(device)
@@ -531,6 +605,10 @@ def main():
         rec["sweep"] = time_sweep(device, args.sweep_images)
     if not args.no_budgets:
         rec["budgets_8b_class"] = time_budgets(device)
+        dense = W.config(4, budget=1.0)
+        rec["compaction_8b_dense"] = dict(
+            what=f"slab fill of {dense.name} at budget 1.0 (every prior row kept)", **time_pack(dense, device))
+        del dense
     if not args.no_peaks:
         rec["measured_peaks"] = measured_peaks(device)
         rec["attention_frac_of_gemm"] = round(achieved / 1e12 / rec["measured_peaks"]["bf16_gemm_8192_tflops"], 4)
