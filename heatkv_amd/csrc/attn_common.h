@@ -312,43 +312,46 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
 //
 // With a workspace, some items are cut into two parts of their key-tile
 // stream so that the launch fills whole rounds of the device's resident
-// workgroup slots G: with G < N < 2G items, the last 2G - N (the lightest, in
-// longest-first order) are cut, giving exactly 2G units and a second round
-// that ends with the first instead of one made of a few leftover items; with
-// N <= G, the first min(N, G - N) (the heaviest) are cut, so the one round is
-// not set by the heaviest item.  N >= 2G launches are not cut.  An item with
-// fewer than 2 kMinPartTiles key tiles still runs whole: its second part
-// finds too few tiles and leaves at once.  A part leaves its partial result (unnormalized O, running max and sum) in a
-// workspace record; the part that completes an item last merges both records
-// in part order.  Workgroup ids: items [0, first) whole, then the cut items'
-// parts, then the remaining items whole.  The parts of a cut item are
-// adjacent when every item has at least 2 kMinPartTiles tiles; otherwise all
-// first parts come before all second parts: workgroup ids are dealt to the 8
-// XCDs round robin, and adjacent second parts that leave at once would leave
-// half of the XCDs idle.  (Measured on the 2B scales: adjacent parts run
-// scale 9 in 36 us against 40 us grouped; grouped parts run scale 8 in 21 us
-// against 30 us adjacent.)
+// workgroup slots G.  Items are numbered longest first.  With G < N < 2G
+// items, the first (heaviest) 2G - N are cut, giving exactly 2G units, and
+// the whole items run first: the second round is then made of halves, so
+// it ends close to the first instead of waiting on heavy items that began
+// in it whole (on the 2B sweep's scale 11, 576 items of 37 to 90 key tiles,
+// a slot model gives 116 us against 133 us for cutting the lightest).  With
+// N <= G, the first min(N, G - N) are cut, so the one round is not set by
+// the heaviest item.  N >= 2G launches are not cut.  An item with fewer than
+// 2 kMinPartTiles key tiles still runs whole: its second part finds too few
+// tiles and leaves at once.  A part leaves its partial result (unnormalized
+// O, running max and sum) in a workspace record; the part that completes an
+// item last merges both records in part order.  Workgroup ids: with
+// whole_first, items [two, N) whole, then the cut items' parts; otherwise
+// the cut items' parts, then items [two, N) whole.  The parts of a cut item
+// are adjacent when every item has at least 2 kMinPartTiles tiles;
+// otherwise all first parts come before all second parts: workgroup ids are
+// dealt to the 8 XCDs round robin, and adjacent second parts that leave at
+// once would leave half of the XCDs idle.  (Measured on the 2B scales:
+// adjacent parts run scale 9 in 36 us against 40 us grouped; grouped parts
+// run scale 8 in 21 us against 30 us adjacent.)
 // Key tiles a part of a cut item must have at least (measured on the 2B
 // scales: parts of ~8.5 tiles gain 13 %, parts of ~5 tiles lose 20 %).
 constexpr int32_t kMinPartTiles = 8;
 
 struct RoundSplit {
-  int32_t items;    // N
-  int32_t first;    // first cut item
-  int32_t two;      // cut items
-  int32_t grouped;  // first parts, then second parts (else each item's two parts adjacent)
+  int32_t items;        // N
+  int32_t two;          // cut items: [0, two) in longest-first order
+  int32_t grouped;      // first parts, then second parts (else each item's two parts adjacent)
+  int32_t whole_first;  // whole items before the cut items' parts
 };
 
 // `min_tiles`: key tiles every item has at least (its current-scale tiles).
 __host__ __device__ __forceinline__ RoundSplit round_split(int32_t items, int32_t slots, int32_t min_tiles) {
-  RoundSplit t{items, 0, 0, min_tiles < 2 * kMinPartTiles ? 1 : 0};
+  RoundSplit t{items, 0, min_tiles < 2 * kMinPartTiles ? 1 : 0, 0};
   if (slots <= 0 || items >= 2 * slots) return t;
   if (items > slots) {
     t.two = 2 * slots - items;
-    t.first = items - t.two;
+    t.whole_first = 1;
   } else {
     t.two = items < slots - items ? items : slots - items;
-    t.first = 0;
   }
   return t;
 }
@@ -368,20 +371,25 @@ struct Unit {
   int32_t counter;  // counter of the item (parts > 1)
 };
 
-__device__ __forceinline__ Unit split_unit(const RoundSplit& t, int32_t j) {
+__host__ __device__ __forceinline__ Unit split_unit(const RoundSplit& t, int32_t j) {
   Unit u{j, 0, 1, 0, 0};
-  if (j < t.first) return u;
-  const int32_t k = j - t.first;
+  if (t.two == 0) return u;
+  const int32_t lead = t.whole_first ? t.items - t.two : 0;  // whole items before the parts
+  if (j < lead) {
+    u.item = t.two + j;
+    return u;
+  }
+  const int32_t k = j - lead;
   if (k < 2 * t.two) {
     const int32_t c = t.grouped ? (k < t.two ? k : k - t.two) : k / 2;  // cut item
-    u.item = t.first + c;
+    u.item = c;
     u.part = t.grouped ? (k < t.two ? 0 : 1) : k % 2;
     u.parts = 2;
     u.record = 2 * c;
     u.counter = c;
     return u;
   }
-  u.item = j - t.two;
+  u.item = k - t.two;  // whole items after the parts: k - 2 two + two
   return u;
 }
 

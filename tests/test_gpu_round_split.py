@@ -2,10 +2,10 @@
 
 With a workspace (the Python operator passes one unless HKV_ATTN_SPLIT=0),
 launches with fewer than two rounds of items per CU slot cut some (batch,
-head, 128-query tile) items into two parts of their key-tile stream: the
-lightest ones when there are between one and two rounds, the heaviest when
-there is at most one; the part that completes an item last merges both
-parts' partial records.  An item with fewer than 16 key tiles runs whole
+head, 128-query tile) items into two parts of their key-tile stream, the
+heaviest ones first (between one and two rounds: 2G - N of them, with the
+whole items issued before the parts; at most one round: min(N, G - N)); the
+part that completes an item last merges both parts' partial records.  An item with fewer than 16 key tiles runs whole
 (its second part leaves at once).  The parts of a cut item are adjacent
 workgroups when the current scale alone gives every item 16 tiles, else all
 first parts precede all second parts.  These cases cover merges of long and
@@ -131,8 +131,8 @@ def test_items_shorter_than_their_parts(device, monkeypatch, L):
 
 
 def test_items_just_above_slots(device, monkeypatch):
-    """slots + 3 items: the 6 heaviest whole, the rest cut in two; heads of
-    mixed retained length."""
+    """slots + 3 items: the slots - 3 heaviest cut in two, the 6 lightest run
+    whole first; heads of mixed retained length."""
     H = _slots(device) + 3
     B, L, cap, S = 1, 100, 3000, 2
     print(f"[split] items just above slots H={H}", flush=True)
@@ -171,7 +171,8 @@ def test_config5_batches_cut(device, monkeypatch):
 
 def test_second_round_of_cut_items(device, monkeypatch):
     """The 2B shape of scale 11 (L = 2304: 576 items for 512 slots on a 256-CU
-    device): the lightest items are cut so the second round is full."""
+    device): the 448 heaviest items are cut, so the second round is made of
+    halves."""
     B, H, L, cap, S = 2, 16, 2304, 6425, 9
     print(f"[split] second round B={B} H={H} L={L}", flush=True)
     g = torch.Generator().manual_seed(61)
