@@ -92,6 +92,9 @@ def parse():
     ap.add_argument("--no-real-model", action="store_true", help="skip the fp32 q/k (model precision) leg")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured GEMM / copy peaks")
     ap.add_argument("--sweep-images", type=int, default=3)
+    ap.add_argument("--pack-only", action="store_true",
+                    help="profiling mode: only the 8B-class budget-1.0 slab fill (12 pack launches per "
+                         "fill); prints its compaction record")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (3 launches) so that a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE pass can scale its counters")
@@ -559,6 +562,14 @@ def main():
     from heatkv_amd import workloads as W
 
     device = torch.device("cuda:0")
+    if args.pack_only:
+        dense = W.config(4, budget=1.0)
+        rec = {"compaction_8b_dense": dict(
+            what=f"slab fill of {dense.name} at budget 1.0 (every prior row kept)", **time_pack(dense, device))}
+        if args.copy_calib_mib > 0:
+            copy_calibration(device, args.copy_calib_mib)
+        print(json.dumps(rec), flush=True)
+        return
     wl = W.config(args.config, budget=args.budget)
     flops = wl.attention_flops()
     kw = attention_call(wl, device)

@@ -10,6 +10,10 @@ Three reports, each written as a short text/JSON file under ``profiles/``:
   in the same run (``bench.py --copy-calib-mib N`` launches it): the copy
   moves N MiB each way, so ``factor = N MiB / counter(copy)``.
 * ``counters`` -- mean per-dispatch values of any other ``--pmc`` counters.
+* ``group``   -- a kernel launched as a fixed group of dispatches (e.g. the
+  12 append launches of one slab fill): summed duration (``--kernel-trace``
+  CSV) and calibrated HBM bytes (as in ``traffic``) per group, against the
+  group's algorithmic bytes.
 
 Usage::
 
@@ -18,6 +22,8 @@ Usage::
         --kernel seg_attn_direct --calib-mib 512 --out profiles/x.json --cmd "..."
     python -m heatkv_amd.rocprof_summary counters C.csv [C2.csv ...] --kernel seg_attn_direct \\
         --out profiles/x.md --cmd "..."
+    python -m heatkv_amd.rocprof_summary group --trace KT_DIR --fetch F.csv --write W.csv \\
+        --kernel pack_kernel --group 12 --algo-bytes N --calib-mib 512 --out profiles/x.json --cmd "..."
 """
 
 from __future__ import annotations
@@ -92,6 +98,28 @@ def traffic(fetch_csv: str, write_csv: str, kernel_substr: str, calib_mib: int, 
     return res
 
 
+def group_summary(trace_dir: str, fetch_csv: str, write_csv: str, kernel_substr: str, group: int,
+                  algo_bytes: int, calib_mib: int, cmd: str) -> dict:
+    """Per group of ``group`` dispatches of ``kernel_substr``: summed kernel
+    time, calibrated HBM bytes, and the bandwidth of the algorithmic bytes."""
+    paths = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise FileNotFoundError(f"no *kernel_trace.csv under {trace_dir}")
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            for r in _rows(paths[0]) if kernel_substr in r["Kernel_Name"]]
+    if len(durs) < group or len(durs) % group:
+        raise ValueError(f"{len(durs)} dispatches of {kernel_substr!r} do not form groups of {group}")
+    groups = len(durs) // group
+    ns = sum(durs) / groups
+    t = traffic(fetch_csv, write_csv, kernel_substr, calib_mib, cmd)
+    hbm = t["bytes_per_dispatch"] * group
+    return {"kernel": kernel_substr, "command": cmd, "dispatches_per_group": group, "groups": groups,
+            "kernel_us_per_group": round(ns / 1e3, 2), "algorithmic_bytes_per_group": int(algo_bytes),
+            "achieved_GBps": round(algo_bytes / ns, 1), "hbm_bytes_per_group": int(hbm),
+            "hbm_over_algorithmic": round(hbm / algo_bytes, 4), "read_factor": t["read_factor"],
+            "write_factor": t["write_factor"]}
+
+
 def counters_markdown(paths: List[str], kernel_substr: str, cmd: str) -> str:
     vals: Dict[str, List[float]] = {}
     for p in paths:
@@ -128,9 +156,22 @@ def main(argv=None):
     c.add_argument("--kernel", required=True)
     c.add_argument("--out", required=True)
     c.add_argument("--cmd", required=True)
+    d = sub.add_parser("group")
+    d.add_argument("--trace", required=True)
+    d.add_argument("--fetch", required=True)
+    d.add_argument("--write", required=True)
+    d.add_argument("--kernel", required=True)
+    d.add_argument("--group", type=int, required=True)
+    d.add_argument("--algo-bytes", type=int, required=True)
+    d.add_argument("--calib-mib", type=int, required=True)
+    d.add_argument("--out", required=True)
+    d.add_argument("--cmd", required=True)
     args = ap.parse_args(argv)
     if args.what == "stats":
         text = stats_markdown(args.kt_dir, args.cmd)
+    elif args.what == "group":
+        text = json.dumps(group_summary(args.trace, args.fetch, args.write, args.kernel, args.group,
+                                        args.algo_bytes, args.calib_mib, args.cmd), indent=1) + "\n"
     elif args.what == "traffic":
         text = json.dumps(traffic(args.fetch, args.write, args.kernel, args.calib_mib, args.cmd), indent=1) + "\n"
     else:
