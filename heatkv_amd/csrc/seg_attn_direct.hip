@@ -346,9 +346,19 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     exp_tile(scur, m_run, sc.c, l_run);
     pack(scur, pf);
     pv(pf, t);
+    // The row sum and the max of a whole S(t + 1) are pinned to this block
+    // (empty asm uses), so the scheduler interleaves them with the PV MFMAs
+    // instead of sinking them past the branch of the rare partial-tile mask,
+    // which then takes the max again (0.8-1 % faster on the 2B and 8B final
+    // steps).
+    asm volatile("" : "+v"(l_run));
+    float mx = tile_max(snext);
+    asm volatile("" : "+v"(mx));
     const int vn = valid_of(t + 1);
-    if (vn < kBN) mask_tile(snext, vn, g);
-    const float mx = tile_max(snext);
+    if (vn < kBN) {
+      mask_tile(snext, vn, g);
+      mx = tile_max(snext);
+    }
     move_max(oacc, m_run, l_run, mx, sc.c, sc.thresh);
   };
   int t = t_begin;
