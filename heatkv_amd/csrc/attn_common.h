@@ -227,6 +227,101 @@ __device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ s
   w.R = seg_pref[nseg];
 }
 
+// plan_work for H <= 64 heads and S <= 64 entries per head, by wave 0 alone
+// with one workgroup barrier: each lane loads table entries (all in flight at
+// once), LDS atomics sum every head's live lengths, lane h ranks head h
+// against the others read lane by lane, a ballot finds the item's head, and
+// a wave scan gives its length prefix.  Same result as the general path
+// below (same clamping, same longest-first order, ties by head index).
+// `bc` receives 3 ints for the other waves.
+__device__ __forceinline__ WorkItem plan_work_small(const int32_t* __restrict__ seg_starts,
+                                                    const int32_t* __restrict__ seg_ends,
+                                                    const int32_t* __restrict__ seg_counts, int64_t cap,
+                                                    int H, int S, int B, int32_t n_qt,
+                                                    int32_t* head_rows, int32_t* bc, int32_t* seg_start,
+                                                    int32_t* seg_pref, int32_t item, int32_t* tab) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int32_t HS = H * S;
+  int32_t* const tab_start = tab;
+  int32_t* const tab_len = tab + HS;
+  int32_t* const tab_cnt = tab + 2 * HS;
+  const int32_t per_rank = B * n_qt;
+  const int32_t target = item / per_rank;
+  if (tid < 64) {
+    int cnt = 0;
+    if (lane < H) {
+      const int n = seg_counts[lane];
+      cnt = n < 0 ? 0 : (n > S ? S : n);
+      tab_cnt[lane] = cnt;
+      head_rows[lane] = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int p0 = 0; p0 < HS; p0 += 8 * 64) {
+      int32_t st[8], en[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int p = p0 + k * 64 + lane;
+        st[k] = p < HS ? seg_starts[p] : 0;
+        en[k] = p < HS ? seg_ends[p] : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int p = p0 + k * 64 + lane;
+        if (p < HS) {
+          int64_t a = st[k], e = en[k];
+          a = a < 0 ? 0 : (a > cap ? cap : a);
+          e = e < 0 ? 0 : (e > cap ? cap : e);
+          const int32_t len = e > a ? static_cast<int32_t>(e - a) : 0;
+          tab_start[p] = static_cast<int32_t>(a);
+          tab_len[p] = len;
+          const int hh = p / S;
+          if (p - hh * S < tab_cnt[hh]) atomicAdd(head_rows + hh, len);
+        }
+      }
+    }
+    // LDS operations of one wave complete in order: the sums are final here
+    __builtin_amdgcn_wave_barrier();
+    const int r = lane < H ? head_rows[lane] : -1;
+    int rank = 0;
+    for (int o = 0; o < H; ++o) {
+      const int ro = __builtin_amdgcn_readlane(r, o);
+      rank += (ro > r) || (ro == r && o < lane);
+    }
+    const uint64_t hit = __ballot(lane < H && rank == target);
+    const int h = hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : 0;  // one lane matches
+    const int nseg = __builtin_amdgcn_readlane(cnt, h);
+    const int len = lane < nseg ? tab_len[h * S + lane] : 0;
+    const int st0 = lane < nseg ? tab_start[h * S + lane] : 0;
+    int incl = len;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane < nseg) {
+      seg_start[lane] = st0;
+      seg_pref[lane + 1] = incl;
+    }
+    if (lane == 0) {
+      seg_pref[0] = 0;
+      bc[0] = h;
+      bc[1] = nseg;
+      bc[2] = nseg > 0 ? __builtin_amdgcn_readlane(incl, nseg - 1) : 0;
+    }
+  }
+  __syncthreads();
+  WorkItem w;
+  const int32_t rem = item - target * per_rank;
+  w.b = rem / n_qt;
+  w.qt = rem - w.b * n_qt;
+  w.h = bc[0];
+  w.bh = w.b * H + w.h;
+  w.nseg = bc[1];
+  w.R = bc[2];
+  return w;
+}
+
 // Longest-first order of the heads, the (b, h, query tile) of item `item`
 // in that order, and head h's clamped segment starts + exclusive length
 // prefix in LDS.  Ends with a workgroup barrier.  head_rows / head_by_rank
@@ -244,6 +339,9 @@ __device__ __forceinline__ WorkItem plan_work(const int32_t* __restrict__ seg_st
   const int tid = threadIdx.x;
   const int32_t HS = H * S;
   const bool in_lds = 2 * HS + H <= tab_ints;
+  if (in_lds && H <= 64 && S <= 64)
+    return plan_work_small(seg_starts, seg_ends, seg_counts, cap, H, S, B, n_qt, head_rows, head_by_rank,
+                           seg_start, seg_pref, item, tab);
   int32_t* const tab_start = tab;
   int32_t* const tab_len = tab + HS;
   int32_t* const tab_cnt = tab + 2 * HS;

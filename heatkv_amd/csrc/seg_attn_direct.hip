@@ -263,6 +263,15 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   };
   auto valid_of = [&](int t) { return t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN); };
 
+  // Q first: its loads are in flight while wave 0 fills the row tables
+  const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
+  u32x4_t qf[8];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * 2, static_cast<uint32_t>(L * kD * 2));
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
+  }
   int cur_seg = 0;
   if (wave == 0) {
     for (int p = t_begin; p < t_begin + 3 && p < ntp && p < t_end; ++p)
@@ -270,18 +279,8 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   }
   __syncthreads();
   issue_tile(t_begin);
-
-  const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
-  u32x4_t qf[8];
-  {
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-        static_cast<const uint8_t*>(a.q) + cur_row0 * kD * 2, static_cast<uint32_t>(L * kD * 2));
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
-      qf[ks] ^= sc.q_sign;
-    }
-  }
+  for (int ks = 0; ks < 8; ++ks) qf[ks] ^= sc.q_sign;
 
   f32x16_t oacc[4];
 #pragma unroll
