@@ -141,7 +141,10 @@ def _random_case(seed, B, H, L, cap, S, *, dtype=torch.bfloat16, kdtype=None, vd
 @pytest.mark.parametrize(
     "seed,B,H,L,cap,S",
     [(11, 1, 2, 1, 50, 3), (12, 2, 3, 5, 200, 5), (13, 1, 4, 33, 300, 7), (14, 2, 2, 130, 97, 4),
-     (15, 1, 1, 257, 1000, 12), (16, 3, 5, 64, 0, 0)],
+     (15, 1, 1, 257, 1000, 12), (16, 3, 5, 64, 0, 0),
+     # work planning: one wave up to 64 heads x 64 entries, all threads beyond
+     (17, 1, 64, 40, 3000, 64), (18, 1, 65, 20, 500, 3), (19, 2, 3, 70, 2000, 65),
+     (20, 1, 2, 10, 100000, 200)],
 )
 def test_attention_random_tables(seed, B, H, L, cap, S, device):
     print(f"[attn] random seed={seed} B={B} H={H} L={L} cap={cap} S={S}", flush=True)
@@ -317,3 +320,17 @@ def test_attention_out_dtype_is_a_single_rounding(qk, out, device):
     assert torch.equal(got, full.to(out))
     with pytest.raises(ValueError, match="out_dtype"):
         fused_real_pruning_flat_segmented_attention(**kw, out_dtype=torch.int32)
+
+
+@pytest.mark.parametrize("H,S", [(16, 40), (3, 70)])
+def test_attention_fp32_qk_random_tables(H, S, device):
+    """fp32 q/k (the register-staged kernel) over random tables on both
+    planning paths (one wave for 16 x 40 entries, all threads for 70)."""
+    print(f"[attn] fp32 q/k random H={H} S={S}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(21 + H, 1, H, 50, 4000, S, kdtype=torch.float32,
+                                             dtype=torch.float32, vdtype=torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"fp32 q/k H={H} S={S}")
