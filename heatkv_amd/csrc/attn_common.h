@@ -668,6 +668,45 @@ __device__ __forceinline__ void write_output(const f32x16_t (&oacc)[4], float m_
   if (lse != nullptr && g == 0) lse[bh * L + qrow] = (m_run * c + __log2f(l_tot)) * 0.6931471805599453f;
 }
 
+// write_output for 16-bit output types through LDS: each wave rounds its
+// 32 x 128 tile into `stage` (32 rows of kOutPitch bytes, private to the
+// wave; the pad spreads the rows over the banks), then stores whole 256-byte
+// rows, 16 lanes per row and 4 rows per instruction (8 full-line stores
+// instead of 16 that each touch 32 rows).  Same values as write_output.
+// `qrow0` is the wave's first query; `out` must be 16-byte aligned.
+constexpr int kOutPitch = kD * 2 + 16;
+template <int DT>
+__device__ __forceinline__ void write_output_lds(const f32x16_t (&oacc)[4], float m_run, float l_run,
+                                                 float c, void* out, float* lse, int64_t b, int64_t h,
+                                                 int32_t qrow0, int L, int H, int64_t bh, int lane,
+                                                 uint8_t* stage) {
+  const int g = lane >> 5;
+  const int q = lane & 31;
+  const float l_tot = pair_sum(l_run);
+  const float inv = 1.f / l_tot;
+  uint8_t* const mine = stage + q * kOutPitch;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      u32x2_t w;
+      w[0] = pack2<DT>(oacc[db][4 * jb + 0] * inv, oacc[db][4 * jb + 1] * inv);
+      w[1] = pack2<DT>(oacc[db][4 * jb + 2] * inv, oacc[db][4 * jb + 3] * inv);
+      *reinterpret_cast<u32x2_t*>(mine + (db * 32 + 8 * jb + 4 * g) * 2) = w;
+    }
+  __builtin_amdgcn_wave_barrier();  // a wave's LDS operations run in order
+  const int64_t row_stride = static_cast<int64_t>(H) * kD;
+  uint16_t* const base = static_cast<uint16_t*>(out) + b * L * row_stride + h * kD + (lane & 15) * 8;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int row = 4 * k + (lane >> 4);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + row * kOutPitch + (lane & 15) * 16);
+    if (qrow0 + row < L) *reinterpret_cast<u32x4_t*>(base + (qrow0 + row) * row_stride) = v;
+  }
+  if (lse != nullptr && g == 0 && qrow0 + q < L)
+    lse[bh * L + qrow0 + q] = (m_run * c + __log2f(l_tot)) * 0.6931471805599453f;
+}
+
 // Launch plumbing shared by the two kernels.
 struct Scalars {
   float c;          // max(|scale| * log2(e), kMinC): the exp2 multiplier, > 0

@@ -385,7 +385,18 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   }
 
   if (parts == 1) {
-    write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+    if (a.out_dtype != kF32 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+      static_assert(NS * kStageBytes >= NW * 32 * kOutPitch, "output staging fits the ring");
+      __syncthreads();  // every wave is past its last tile: the ring is free
+      uint8_t* const stage = ring + wave * 32 * kOutPitch;
+      const int32_t qrow0 = w.qt * kBM + wave * 32;
+      if (a.out_dtype == kF16)
+        write_output_lds<kF16>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, lane, stage);
+      else
+        write_output_lds<kBF16>(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, lane, stage);
+    } else {
+      write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+    }
     return;
   }
   merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);
