@@ -97,7 +97,7 @@ template <int QDT, int kThreads>
 __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc, const Unit& un,
                                             int32_t parts, const f32x16_t (&oacc)[4], float m_run,
                                             float l_run, const WorkItem& w, int32_t qrow, int L, int H,
-                                            int g, int32_t& merge_turn) {
+                                            int g, int32_t& merge_turn, uint8_t* stage) {
   const int tid = threadIdx.x;
   int32_t* const counters = static_cast<int32_t*>(a.workspace);
   float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
@@ -156,7 +156,16 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
     }
     l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
   }
-  write_output(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+  if (a.out_dtype != kF32 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+    // the ring is free: every wave passed the barriers above after its last tile
+    const int32_t qrow0 = qrow - (tid & 31);
+    if (a.out_dtype == kF16)
+      write_output_lds<kF16>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, tid & 63, stage);
+    else
+      write_output_lds<kBF16>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, tid & 63, stage);
+  } else {
+    write_output(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+  }
   if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -399,7 +408,8 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     }
     return;
   }
-  merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn);
+  merge_parts<QDT, kThreads>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn,
+                             ring + wave * 32 * kOutPitch);
 }
 
 // Resident workgroups of the kernel (2 per CU) on `device`, cached.
