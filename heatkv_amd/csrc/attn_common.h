@@ -230,10 +230,11 @@ __device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ s
 // plan_work for H <= 64 heads and S <= 64 entries per head, by wave 0 alone
 // with one workgroup barrier: each lane loads table entries (all in flight at
 // once), LDS atomics sum every head's live lengths, lane h ranks head h
-// against the others read lane by lane, a ballot finds the item's head, and
-// a wave scan gives its length prefix.  Same result as the general path
-// below (same clamping, same longest-first order, ties by head index).
-// `bc` receives 3 ints for the other waves.
+// against the others (read from LDS 16 at a time), a ballot finds the
+// item's head, and a wave scan gives its length prefix.  Same result as the
+// general path below (same clamping, same longest-first order, ties by head
+// index).
+// `bc` receives 3 ints for the other waves; head_rows is 16-byte aligned.
 __device__ __forceinline__ WorkItem plan_work_small(const int32_t* __restrict__ seg_starts,
                                                     const int32_t* __restrict__ seg_ends,
                                                     const int32_t* __restrict__ seg_counts, int64_t cap,
@@ -284,9 +285,22 @@ __device__ __forceinline__ WorkItem plan_work_small(const int32_t* __restrict__ 
     __builtin_amdgcn_wave_barrier();
     const int r = lane < H ? head_rows[lane] : -1;
     int rank = 0;
-    for (int o = 0; o < H; ++o) {
-      const int ro = __builtin_amdgcn_readlane(r, o);
-      rank += (ro > r) || (ro == r && o < lane);
+    const int4* const hr4 = reinterpret_cast<const int4*>(head_rows);
+    for (int o0 = 0; o0 < H; o0 += 16) {  // 16 rows per LDS round trip
+      int v[16];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int4 x = hr4[o0 / 4 + k];
+        v[4 * k + 0] = x.x;
+        v[4 * k + 1] = x.y;
+        v[4 * k + 2] = x.z;
+        v[4 * k + 3] = x.w;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int o = o0 + k;
+        rank += o < H && ((v[k] > r) || (v[k] == r && o < lane));
+      }
     }
     const uint64_t hit = __ballot(lane < H && rank == target);
     const int h = hit != 0 ? static_cast<int>(__builtin_ctzll(hit)) : 0;  // one lane matches

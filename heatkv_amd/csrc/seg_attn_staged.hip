@@ -44,7 +44,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   __shared__ __attribute__((aligned(16))) int32_t rowtab[2][kBN];
   __shared__ int32_t seg_start[kMaxSegments];
   __shared__ int32_t seg_pref[kMaxSegments + 1];
-  __shared__ int32_t head_rows[kMaxHeads];
+  __shared__ __attribute__((aligned(16))) int32_t head_rows[kMaxHeads];
   __shared__ int32_t head_by_rank[kMaxHeads];
 
   const int64_t cap = a.slab_capacity;
