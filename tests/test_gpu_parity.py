@@ -334,3 +334,41 @@ def test_attention_fp32_qk_random_tables(H, S, device):
     ref_out, ref_lse = oattn.flat_segmented_attention(
         to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
     assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"fp32 q/k H={H} S={S}")
+
+
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_attention_output_not_16_byte_aligned(split, device, monkeypatch):
+    """16-bit output through the C ABI at an address 8 bytes past 16-byte
+    alignment: the kernel then stores from registers instead of staging
+    rows in LDS, with the same bits (whole items and, with the workspace,
+    merged parts)."""
+    from heatkv_amd import _lib
+
+    monkeypatch.setenv("HKV_ATTN_SPLIT", split)
+    B, H, L, cap, S = 1, 4, 200, 3000, 1
+    print(f"[attn] unaligned output split={split}", flush=True)
+    q, sk, sv, _, ck, cv = _random_case(31, B, H, L, cap, 0)
+    # every head keeps the whole slab: 51 key tiles per item, so with the
+    # workspace the 8 items are cut into parts and merged
+    st = torch.zeros((H, S), dtype=torch.int32, device=device)
+    en = torch.full((H, S), cap, dtype=torch.int32, device=device)
+    ct = torch.ones((H,), dtype=torch.int32, device=device)
+    scale = 1.0 / math.sqrt(128)
+    qd, skd, svd, ckd, cvd = (t.to(device) for t in (q, sk, sv, ck, cv))
+    want = fused_real_pruning_flat_segmented_attention(
+        q=qd, persisted_k=skd, persisted_v=svd, segment_starts=st, segment_ends=en, segment_counts=ct,
+        current_k=ckd, current_v=cvd, softmax_scale=scale)
+    buf = torch.zeros(B * L * H * 128 + 4, dtype=torch.bfloat16, device=device)
+    assert (buf.data_ptr() + 8) % 16 == 8
+    ws = _lib.attention_workspace(device) if split == "1" else None
+    stream = torch.cuda.current_stream(device)
+    code = _lib.load().hkv_segmented_attention(
+        qd.data_ptr(), skd.data_ptr(), svd.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
+        ckd.data_ptr(), cvd.data_ptr(), buf.data_ptr() + 8, None, B, H, L, cap, S, 128,
+        _lib.dtype_code(qd.dtype), _lib.dtype_code(ckd.dtype), _lib.dtype_code(cvd.dtype), 0, float(scale), 0,
+        ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
+        stream.cuda_stream)
+    _lib.check(code)
+    torch.cuda.synchronize(device)
+    got = buf[4:].reshape(B, L, H * 128)
+    assert np.array_equal(bits(got), bits(want))
