@@ -372,3 +372,27 @@ def test_attention_output_not_16_byte_aligned(split, device, monkeypatch):
     torch.cuda.synchronize(device)
     got = buf[4:].reshape(B, L, H * 128)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("seed", list(range(40, 52)))
+def test_attention_random_shapes(seed, device, monkeypatch):
+    """Random batch, head count (1-70), table width (0-70), query length and
+    slab size, with and without the round split: both planning paths, cut
+    and whole items, partial tiles, against the oracle."""
+    g = torch.Generator().manual_seed(seed)
+
+    def pick(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    B, H, L, cap, S = pick(1, 3), pick(1, 70), pick(1, 300), pick(0, 5000), pick(0, 70)
+    if cap == 0:
+        S = 0
+    split = "1" if seed % 2 else "0"
+    monkeypatch.setenv("HKV_ATTN_SPLIT", split)
+    print(f"[attn] random shape seed={seed} B={B} H={H} L={L} cap={cap} S={S} split={split}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(seed, B, H, L, cap, S)
+    scale = 1.0 / math.sqrt(128)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"seed {seed}")
