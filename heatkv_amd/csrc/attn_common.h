@@ -250,14 +250,21 @@ __device__ __forceinline__ WorkItem plan_work_small(const int32_t* __restrict__ 
   const int32_t per_rank = B * n_qt;
   const int32_t target = item / per_rank;
   if (tid < 64) {
+    // the counts are clamped and go to LDS after the first batch of table
+    // reads is issued, so that both arrive in one memory round trip
+    const int n_raw = lane < H ? seg_counts[lane] : 0;
     int cnt = 0;
-    if (lane < H) {
-      const int n = seg_counts[lane];
+    auto publish_counts = [&]() {
+      int n = n_raw;
+      asm volatile("" : "+v"(n));  // not before the reads issued above it
       cnt = n < 0 ? 0 : (n > S ? S : n);
-      tab_cnt[lane] = cnt;
-      head_rows[lane] = 0;
-    }
-    __builtin_amdgcn_wave_barrier();
+      if (lane < H) {
+        tab_cnt[lane] = cnt;
+        head_rows[lane] = 0;
+      }
+      __builtin_amdgcn_wave_barrier();
+    };
+    if (HS == 0) publish_counts();
     for (int p0 = 0; p0 < HS; p0 += 8 * 64) {
       int32_t st[8], en[8];
 #pragma unroll
@@ -266,6 +273,7 @@ __device__ __forceinline__ WorkItem plan_work_small(const int32_t* __restrict__ 
         st[k] = p < HS ? seg_starts[p] : 0;
         en[k] = p < HS ? seg_ends[p] : 0;
       }
+      if (p0 == 0) publish_counts();
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int p = p0 + k * 64 + lane;
