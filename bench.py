@@ -4,8 +4,8 @@ One step = one ``fused_real_pruning_flat_segmented_attention`` call of the
 final 64x64 scale (B=2, H=16, D=128, 4096 queries, budget-0.1 slab over the
 6425-token prior, seed 1) with its inputs resident in HBM.  The slab is packed
 once before timing (the final scale appends nothing).  ``--warmup`` untimed
-steps (the default 50 covers the GPU's clock ramp from idle: the first ~40
-launches on a fresh box run up to 20 % slower), then ``--steps`` back-to-back
+steps, after an untimed clock ramp of ``--ramp-ms`` GPU milliseconds of the
+same step, then ``--steps`` back-to-back
 steps between two HIP events recorded on the stream the kernel runs on;
 prints one JSON line.
 
@@ -52,8 +52,15 @@ prints one JSON line.
   same run: a bf16 8192^3 GEMM (torch.matmul, hipBLASLt) in TFLOP/s and a
   1 GiB device copy in GB/s (read + write), beside the nominal 2.5 PF / 8 TB/s;
   ``attention_frac_of_gemm`` relates the attention to the former.
-* ``cpu_baseline``: the numpy fp32 oracle (the reference CPU path's gather +
-  softmax, restated) on the host cores over whole steps, rank 0 only.
+* ``skewed_ragged``: the skewed-ragged final step (B=16, H=16, seed 3,
+  retained lengths log-uniform in [0, 6425]) as its own leg.
+* ``cpu_baseline``: the reference CPU path restated in torch (gather +
+  scaled_dot_product_attention, fp32) on the host cores over whole steps
+  (median of 5 after a warm-up), rank 0 only; ``cores`` = the threads used
+  (the per-GPU CPU share), ``host_cpu_count`` = what the OS reports.
+* ``clock_ramp_ms``: untimed GPU time of the headline step run before its
+  ``--warmup`` (default 300 ms: a cold GPU ramps its clock during the first
+  few hundred milliseconds of load).
 """
 
 from __future__ import annotations
@@ -83,8 +90,11 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5],
                     help="final-step workload (2 = the 2B 1024^2 final scale)")
     ap.add_argument("--budget", type=float, default=None, help="keep budget (configs 1, 2, 4)")
+    ap.add_argument("--ramp-ms", type=float, default=300.0,
+                    help="untimed GPU milliseconds of the headline step before its warmup (clock ramp)")
+    ap.add_argument("--no-skewed", action="store_true", help="skip the skewed-ragged final step (B=16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-repeats", type=int, default=10)
+    ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true", help="skip the 32-layer generation sweep")
     ap.add_argument("--no-budgets", action="store_true",
                     help="skip the 8B-class budget sweep (B=8, H=32, budgets 0.05/0.1/0.2/1.0)")
@@ -112,8 +122,33 @@ def attention_call(wl, device):
                 segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale)
 
 
+def clock_ramp(fn, device, min_ms=300.0, max_wall_s=5.0, chunk=50):
+    """Untimed launches of ``fn`` until at least ``min_ms`` of GPU time has run
+    (bounded by ``max_wall_s`` of wall time): the GPU leaves its idle clocks
+    during the first few hundred milliseconds of load, so a short timed region
+    that starts cold measures the ramp rather than the kernel.  Returns the
+    GPU milliseconds spent and the launches made."""
+    import torch
+
+    stream = torch.cuda.current_stream(device)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    spent, launches = 0.0, 0
+    wall0 = time.perf_counter()
+    while spent < min_ms and time.perf_counter() - wall0 < max_wall_s:
+        e0.record(stream)
+        for _ in range(chunk):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize(device)
+        spent += e0.elapsed_time(e1)
+        launches += chunk
+    return spent, launches
+
+
 def time_attention(kw, device, steps, warmup):
-    """Milliseconds per step over ``steps`` back-to-back calls (HIP events on the kernel's stream)."""
+    """Milliseconds per step over ``steps`` back-to-back calls (HIP events on
+    the kernel's stream) after ``warmup`` untimed calls."""
     import torch
 
     from heatkv_amd import fused_real_pruning_flat_segmented_attention as attn
@@ -444,6 +479,26 @@ def measured_peaks(device):
             "nominal_bf16_tflops": PEAK_BF16_FLOPS / 1e12, "nominal_hbm_GBps": PEAK_HBM_BPS / 1e9}
 
 
+def time_final_step(config, device, steps=20, warmup=10):
+    """One final-step workload (by config number) as its own leg: ms per step,
+    TFLOP/s and the fraction of the bf16 peak."""
+    import torch
+
+    from heatkv_amd import workloads as W
+
+    wl = W.config(config)
+    kw = attention_call(wl, device)
+    ms, _ = time_attention(kw, device, steps, warmup)
+    flops = wl.attention_flops()
+    rows = wl.retained_rows()
+    del kw
+    torch.cuda.empty_cache()
+    return {"workload": wl.name, "batch": wl.batch, "heads": wl.heads, "seed": wl.seed,
+            "retained_rows_min_max": [min(rows), max(rows)], "ms_per_step": round(ms, 4),
+            "flops_per_step": flops, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_bf16_peak": round(flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 4)}
+
+
 def time_budgets(device, steps=20, warmup=10):
     """The 8B-class final step (B=8, H=32, seed 2) at keep budgets 0.05, 0.1,
     0.2 and 1.0 (the unpruned, dense-equivalent case): ms per step and TFLOP/s."""
@@ -479,64 +534,71 @@ def copy_calibration(device, mib):
     torch.cuda.synchronize(device)
 
 
-def cpu_baseline(wl, repeats):
-    """Numpy oracle (fp32) over whole steps on the host cores."""
-    import numpy as np
+def _host_slab(wl):
+    """The slab as the host sees it: each live segment's rows at its offset (fp32)."""
+    import torch
 
+    B, H, _, D = wl.prior_k.shape
+    slab_k = torch.zeros((B, wl.schedule.capacity, D), dtype=torch.float32)
+    slab_v = torch.zeros_like(slab_k)
+    for seg in wl.schedule.live_segments(wl.target):
+        slab_k[:, seg.offset:seg.offset + seg.length] = wl.prior_k[:, seg.head, seg.scale_start:seg.scale_end].float()
+        slab_v[:, seg.offset:seg.offset + seg.length] = wl.prior_v[:, seg.head, seg.scale_start:seg.scale_end].float()
+    return slab_k, slab_v
+
+
+def _cpu_model():
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
+
+
+def cpu_baseline(wl, repeats):
+    """The reference CPU path restated in torch (per (b, h): gather the head's
+    slab segments, append the current K/V, scaled_dot_product_attention, in
+    fp32) on the host cores: 1 warm-up, then the median of ``repeats`` whole
+    steps, for the headline workload and the 7-scale CPU-plumbing workload."""
+    import torch
+
+    from heatkv_amd import workloads as W
     from oracle import segmented_attention as oattn
 
-    try:
-        from threadpoolctl import threadpool_info
+    host_cpus = os.cpu_count() or 1
+    # the pool's CPU share per GPU is 16 threads (OMP_NUM_THREADS there)
+    threads = max(1, min(host_cpus, int(os.environ.get("OMP_NUM_THREADS", host_cpus))))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
 
-        threads = max([int(p.get("num_threads", 1)) for p in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    f = lambda t: t.float().numpy()  # noqa: E731
-    st, en, ct = (t.numpy() for t in wl.tables())
-    # slab as the host sees it: each live segment's rows at its offset
-    B, H, _, D = wl.prior_k.shape
-    slab_k = np.zeros((B, wl.schedule.capacity, D), np.float32)
-    slab_v = np.zeros_like(slab_k)
-    pk, pv = f(wl.prior_k), f(wl.prior_v)
-    for seg in wl.schedule.live_segments(wl.target):
-        slab_k[:, seg.offset:seg.offset + seg.length] = pk[:, seg.head, seg.scale_start:seg.scale_end]
-        slab_v[:, seg.offset:seg.offset + seg.length] = pv[:, seg.head, seg.scale_start:seg.scale_end]
-    args = (f(wl.q), slab_k, slab_v, st, en, ct, f(wl.cur_k), f(wl.cur_v), wl.softmax_scale)
-    oattn.flat_segmented_attention(*args, heads=[0], batches=[0])  # warm-up
-    times = []
-    for _ in range(repeats):
-        t = time.perf_counter()
-        oattn.flat_segmented_attention(*args)
-        times.append(time.perf_counter() - t)
-    sec = statistics.median(times)
-    from heatkv_amd import workloads as W
+    def median_ms(w, reps):
+        st, en, ct = (t.numpy() for t in w.tables())
+        sk, sv = _host_slab(w)
+        args = (w.q, sk, sv, st, en, ct, w.cur_k, w.cur_v, w.softmax_scale)
+        oattn.flat_segmented_attention_sdpa(*args)  # warm-up
+        times = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            oattn.flat_segmented_attention_sdpa(*args)
+            times.append(time.perf_counter() - t)
+        return statistics.median(times) * 1e3
 
-    w1 = W.config(1)
-    st1, en1, ct1 = (t.numpy() for t in w1.tables())
-    s1_k = np.zeros((w1.batch, w1.schedule.capacity, 128), np.float32)
-    s1_v = np.zeros_like(s1_k)
-    for seg in w1.schedule.live_segments(w1.target):
-        s1_k[:, seg.offset:seg.offset + seg.length] = f(w1.prior_k)[:, seg.head, seg.scale_start:seg.scale_end]
-        s1_v[:, seg.offset:seg.offset + seg.length] = f(w1.prior_v)[:, seg.head, seg.scale_start:seg.scale_end]
-    args1 = (f(w1.q), s1_k, s1_v, st1, en1, ct1, f(w1.cur_k), f(w1.cur_v), w1.softmax_scale)
-    oattn.flat_segmented_attention(*args1)
-    t1 = []
-    for _ in range(5):
-        t = time.perf_counter()
-        oattn.flat_segmented_attention(*args1)
-        t1.append(time.perf_counter() - t)
-    model = "unknown"
     try:
-        with open("/proc/cpuinfo") as fh:
-            model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), model)
-    except OSError:
-        pass
-    return dict(value=round(wl.attention_flops() / sec / 1e12, 4), unit="TFLOP/s", cores=threads,
-                cpu_model=model, config1_ms_per_step=round(statistics.median(t1) * 1e3, 3),
-                kind="port",
-                sample=f"{repeats} whole steps of {wl.name} (B={wl.batch}, H={wl.heads}, "
-                       f"L={wl.cur_len}), numpy fp32 oracle, median",
-                ms_per_step=round(sec * 1e3, 2))
+        ms = median_ms(wl, repeats)
+        ms1 = median_ms(W.config(1), max(repeats, 5))
+    finally:
+        torch.set_num_threads(prev)
+    return dict(value=round(wl.attention_flops() / (ms * 1e-3) / 1e12, 4), unit="TFLOP/s", cores=threads,
+                host_cpu_count=host_cpus, cpu_model=_cpu_model(), kind="port",
+                sample=f"{repeats} whole steps of {wl.name} (B={wl.batch}, H={wl.heads}, L={wl.cur_len}) "
+                       "after 1 warm-up, median; torch gather + scaled_dot_product_attention in fp32 "
+                       "(the reference CPU path restated)",
+                ms_per_step=round(ms, 2), config1_ms_per_step=round(ms1, 3))
 
 
 def measured_traffic(kernel: str, workload: str):
@@ -573,6 +635,9 @@ def main():
     wl = W.config(args.config, budget=args.budget)
     flops = wl.attention_flops()
     kw = attention_call(wl, device)
+    from heatkv_amd import fused_real_pruning_flat_segmented_attention as attn
+
+    ramp_ms, ramp_launches = clock_ramp(lambda: attn(**kw), device, args.ramp_ms)
     ms_step, host_us = time_attention(kw, device, args.steps, args.warmup)
     achieved = flops / (ms_step * 1e-3)
     pack = time_pack(wl, device)
@@ -604,10 +669,14 @@ def main():
             "traffic": measured_traffic(ATTN_KERNEL, wl.name),
             "kernel": ATTN_KERNEL, "kernel_ms_mean": round(ms_step, 5),
         },
+        "clock_ramp_ms": round(ramp_ms, 1),
+        "clock_ramp_launches": ramp_launches,
         "host_us_per_call": round(host_us, 1),
         "compaction": dict(what=f"slab fill of {wl.name}: one append launch per kept prior scale",
                            **pack),
     }
+    if not args.no_skewed:
+        rec["skewed_ragged"] = time_final_step(5, device)
     if not args.no_producer:
         rec["producer"] = time_producer(device)
     if not args.no_real_model:

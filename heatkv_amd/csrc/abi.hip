@@ -111,8 +111,13 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
                                 int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
                                 int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                int32_t qk_dot_mode, int32_t value_dot_mode,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
+  if (qk_dot_mode < 0 || qk_dot_mode > 2)
+    return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
+  if (value_dot_mode != 0 && value_dot_mode != 2)
+    return fail(HKV_ERR_INVALID_ARG, "value_dot_mode must be 0 (bf16) or 2 (fp32) (got %d)", value_dot_mode);
   if (head_dim != 128)
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented v1 only supports head_dim=128");
   if (cur_len <= 0)
@@ -181,6 +186,8 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   a.k_dtype = k_dtype;
   a.v_dtype = v_dtype;
   a.out_dtype = out_dtype;
+  a.qk_dot_mode = qk_dot_mode;
+  a.value_dot_mode = value_dot_mode;
   a.workspace = workspace;
   a.workspace_bytes = workspace != nullptr ? workspace_bytes : 0;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));

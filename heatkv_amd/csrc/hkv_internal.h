@@ -31,6 +31,11 @@ hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
 enum Dtype : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3 };
 
+// Dot modes of the reference's REAL_PRUNING_FUSED_QK_DOT_MODE /
+// REAL_PRUNING_FUSED_VALUE_DOT_MODE knobs (0 = default, 1 = TF32 (QK only),
+// 2 = fp32 / IEEE).
+enum DotMode : int32_t { kDotDefault = 0, kDotTf32 = 1, kDotFp32 = 2 };
+
 struct AttnArgs {
   const void* q;
   const void* slab_k;
@@ -52,6 +57,8 @@ struct AttnArgs {
   int32_t k_dtype;
   int32_t v_dtype;
   int32_t out_dtype;        // element type of `out` (q_dtype by default)
+  int32_t qk_dot_mode;      // DotMode of S = Q K^T
+  int32_t value_dot_mode;   // DotMode of O = P V (kDotTf32 not used)
   void* workspace;          // round-split storage, or null
   int64_t workspace_bytes;
 };

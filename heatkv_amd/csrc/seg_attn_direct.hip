@@ -456,7 +456,9 @@ int64_t split_workspace_bytes(int32_t slots) {
 bool attention_direct_supported(const AttnArgs& a) {
   const bool k16 = a.k_dtype == kBF16 || a.k_dtype == kF16;
   const bool v16 = a.v_dtype == kBF16 || a.v_dtype == kF16;
-  return k16 && v16 && a.q_dtype == a.k_dtype && a.heads <= attn::kMaxHeads;
+  // 16-bit q/k products are exact in every QK dot mode; an fp32 P V product
+  // (value mode 2) needs the staged kernel's split P
+  return k16 && v16 && a.q_dtype == a.k_dtype && a.heads <= attn::kMaxHeads && a.value_dot_mode != kDotFp32;
 }
 
 hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream) {

@@ -1,17 +1,30 @@
 // Segmented attention, register-staged variant: serves any mix of fp16 /
-// bf16 / fp32 inputs (fp32 K or V are converted to bf16 MFMA operands while
-// staging, which the direct-to-LDS variant cannot do).  fp32 q and k are
-// split into bf16 high and low parts and S = K Q^T is taken as
-// Kh Qh + Kl Qh + Kh Ql (three MFMAs per step, ~16 significand bits, beyond
-// the TF32 products the reference's Triton dot uses for fp32 operands); fp32
-// V and P are rounded to bf16 for O = P V.
+// bf16 / fp32 inputs and the reference's higher-precision dot modes, which
+// the direct-to-LDS variant (16-bit operands straight from HBM) cannot.
+//
+// Precision by operand splitting.  A value x is written as NP bf16 pieces,
+// x = x0 + x1 + ... with x0 = bf16(x), x1 = bf16(x - x0), ... (each
+// subtraction is exact in fp32), so 2 pieces carry about 16 significand
+// bits and 3 pieces all 24 of fp32.  A product of split operands is taken as
+// the MFMA sum of the piece products a_i b_j with i + j < order (order = the
+// larger piece count), which drops only terms below 2^-8(order) relative:
+//  * QK: fp32 q/k are split in 2 pieces (3 products, ~16 bits; the
+//    reference's default Triton dot of fp32 operands runs at TF32, 11 bits),
+//    or 3 pieces under REAL_PRUNING_FUSED_QK_DOT_MODE=fp32/ieee (6 products,
+//    fp32 accuracy).  16-bit q/k products are exact in every mode.
+//  * PV: by default P is rounded to V's 16-bit type (the reference's
+//    p.to(v.dtype)); with fp32 V the reference keeps P in fp32 and takes a
+//    TF32 dot, here P and V are split in 2 pieces (3 products).  Under
+//    REAL_PRUNING_FUSED_VALUE_DOT_MODE=fp32 (an fp32 P V product) P is split
+//    in 3 pieces and V in as many as its type needs (bf16 1, fp16 2 -- both
+//    exact -- and fp32 3).
 //
 // Each thread loads its share of the next 64-key tile into registers with
 // 16-byte buffer loads (out-of-range rows read as zeros) while the current
-// tile is computed, then stores it to LDS: K row-major with a 272-byte pitch
-// (conflict-free 16-byte operand reads), V transposed to V^T[d][key] with a
-// 136-byte pitch (conflict-free 8-byte operand reads) by a 4x8 register
-// transpose of 16-bit values.
+// tile is computed, then stores it to LDS: K pieces row-major with a 272-byte
+// pitch (conflict-free 16-byte operand reads), V pieces transposed to
+// V^T[d][key] with a 136-byte pitch (conflict-free 8-byte operand reads) by
+// a 4x8 register transpose of 16-bit values.
 #include "attn_common.h"
 
 namespace hkv {
@@ -22,12 +35,95 @@ using namespace attn;
 constexpr int kKPitch = kD * 2 + 16;   // bytes per K row in LDS
 constexpr int kVtPitch = kBN * 2 + 8;  // bytes per V^T row in LDS
 
-template <int QDT, int KDT, int VDT, int NW>
-__global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnArgs a,
-                                                                     const Scalars sc,
-                                                                     const int32_t n_qt) {
-  constexpr int MQK = (QDT == kF16 && KDT == kF16) ? kF16 : kBF16;
-  constexpr int MV = (VDT == kF16) ? kF16 : kBF16;
+// Splits 8 fp32 values into NP packed operand pieces: bf16 pieces when
+// NP > 1, else one piece of type MT (round to nearest even).
+template <int MT, int NP>
+__device__ __forceinline__ void split8(const float (&v)[8], u32x4_t (&out)[NP]) {
+  if constexpr (NP == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[0][i] = pack2<MT>(v[2 * i], v[2 * i + 1]);
+  } else {
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = v[i];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = pack2<kBF16>(r[2 * i], r[2 * i + 1]);
+        out[p][i] = w;
+        if (p + 1 < NP) {
+          r[2 * i] -= __builtin_bit_cast(float, w << 16);
+          r[2 * i + 1] -= __builtin_bit_cast(float, w & 0xffff0000u);
+        }
+      }
+    }
+  }
+}
+
+// 8 consecutive elements of type DT at byte offset `off` of `r` as NP
+// operand pieces (see split8); NP == 1 keeps the plain load8 conversion.
+// An offset of -1 yields zeros.
+template <int DT, int MT, int NP>
+__device__ __forceinline__ void load8_pieces(__amdgpu_buffer_rsrc_t r, int32_t off, u32x4_t (&out)[NP]) {
+  if constexpr (NP == 1) {
+    out[0] = load8<DT, MT>(r, off);
+  } else {
+    float v[8];
+    if constexpr (DT == kF32) {
+      const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+      const f32x4_t y = __builtin_bit_cast(
+          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = x[i];
+        v[4 + i] = y[i];
+      }
+    } else {
+      const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == kF16) {
+          v[2 * i] = f16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+          v[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(w[i] >> 16));
+        } else {
+          v[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+          v[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+        }
+      }
+    }
+    split8<kBF16, NP>(v, out);
+  }
+}
+
+// Piece products of a split contraction step: (i, j) with i + j < ORDER.
+template <int NA, int NB>
+struct Products {
+  static constexpr int kOrder = NA > NB ? NA : NB;
+};
+
+template <int MT, int NA, int NB>
+__device__ __forceinline__ f32x16_t mfma_split(const u32x4_t (&a)[NA], const u32x4_t (&b)[NB], f32x16_t c) {
+  constexpr int order = Products<NA, NB>::kOrder;
+  // largest products first: pieces fall by 2^-8 each
+#pragma unroll
+  for (int s = 0; s < order; ++s)
+#pragma unroll
+    for (int i = 0; i <= s; ++i) {
+      const int j = s - i;
+      if (i < NA && j < NB) c = mfma32<MT>(a[i], b[j], c);
+    }
+  return c;
+}
+
+// NQS: q/k pieces; NPS / NVS: P / V pieces.  MQK / MV: operand types of
+// one-piece products.
+template <int QDT, int KDT, int VDT, int NQS, int NPS, int NVS, int NW, int MINB>
+__global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const AttnArgs a,
+                                                                        const Scalars sc,
+                                                                        const int32_t n_qt) {
+  constexpr int MQK = (NQS == 1 && QDT == kF16 && KDT == kF16) ? kF16 : kBF16;
+  constexpr int MV = (NPS == 1 && NVS == 1 && VDT == kF16) ? kF16 : kBF16;
   constexpr int kThreads = NW * 64;
   constexpr int kBM = NW * 32;
   constexpr int kQuadChunks = kBN / 4 * 16;  // (4-key quad, 16-byte d-chunk) pairs per tensor
@@ -35,12 +131,14 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   constexpr int kEK = KDT == kF32 ? 4 : 2;
   constexpr int kEV = VDT == kF32 ? 4 : 2;
   constexpr int kEQ = QDT == kF32 ? 4 : 2;
-  constexpr bool kSplit = QDT == kF32 && KDT == kF32;
+  constexpr int kKBytes = kBN * kKPitch;
+  constexpr int kVBytes = kD * kVtPitch;
+  constexpr int kNL = NQS > NVS ? NQS : NVS;  // pieces held per staged load
   static_assert(2 * kQuadChunks % kThreads == 0, "loader split");
+  static_assert(NQS >= 1 && NQS <= 3 && NPS >= 1 && NPS <= 3 && NVS >= 1 && NVS <= 3, "pieces");
 
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[kBN * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds_lo[kSplit ? kBN * kKPitch : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kD * kVtPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[NQS * kKBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[NVS * kVBytes];
   __shared__ __attribute__((aligned(16))) int32_t rowtab[2][kBN];
   __shared__ int32_t seg_start[kMaxSegments];
   __shared__ int32_t seg_pref[kMaxSegments + 1];
@@ -79,47 +177,40 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   int cur_seg = 0;
   // quad-chunk i covers keys 4(i/16)..+3 at d 8(i%16)..+7 of K (i < kQuadChunks)
   // or of V; thread tid owns quad-chunks tid, tid + kThreads, ...
-  u32x4_t lreg[kLoadsPerThread][4];
-  u32x4_t lreg_lo[kSplit ? kLoadsPerThread : 1][4];  // low bf16 parts of fp32 K
-  auto issue_loads = [&](int tile, int buf) {
-    if (tile < ntp) {
+  u32x4_t lreg[kLoadsPerThread][4][kNL];
+  auto load_row = [&](bool is_v, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int32_t row, int lc,
+                      u32x4_t (&dst)[kNL]) {
+    if (is_v) {
+      u32x4_t p[NVS];
+      load8_pieces<VDT, MV, NVS>(rv, row < 0 ? -1 : (row * kD + lc * 8) * kEV, p);
 #pragma unroll
-      for (int it = 0; it < kLoadsPerThread; ++it) {
-        const int item = tid + it * kThreads;
-        const bool is_v = item >= kQuadChunks;
-        const int qc = is_v ? item - kQuadChunks : item;
-        const int lq = qc >> 4;
-        const int lc = qc & 15;
+      for (int i = 0; i < NVS; ++i) dst[i] = p[i];
+    } else {
+      u32x4_t p[NQS];
+      load8_pieces<KDT, MQK, NQS>(rk, row < 0 ? -1 : (row * kD + lc * 8) * kEK, p);
+#pragma unroll
+      for (int i = 0; i < NQS; ++i) dst[i] = p[i];
+    }
+  };
+  auto issue_loads = [&](int tile, int buf) {
+#pragma unroll
+    for (int it = 0; it < kLoadsPerThread; ++it) {
+      const int item = tid + it * kThreads;
+      const bool is_v = item >= kQuadChunks;
+      const int qc = is_v ? item - kQuadChunks : item;
+      const int lq = qc >> 4;
+      const int lc = qc & 15;
+      if (tile < ntp) {
         const int4 rows = *reinterpret_cast<const int4*>(&rowtab[buf][lq * 4]);
         const int rr[4] = {rows.x, rows.y, rows.z, rows.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (is_v)
-            lreg[it][i] = load8<VDT, MV>(rs_v, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEV);
-          else if constexpr (kSplit)
-            load8_split(rs_k, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEK, lreg[it][i], lreg_lo[it][i]);
-          else
-            lreg[it][i] = load8<KDT, MQK>(rs_k, rr[i] < 0 ? -1 : (rr[i] * kD + lc * 8) * kEK);
-        }
-      }
-    } else {
-      const int row0 = (tile - ntp) * kBN;
-#pragma unroll
-      for (int it = 0; it < kLoadsPerThread; ++it) {
-        const int item = tid + it * kThreads;
-        const bool is_v = item >= kQuadChunks;
-        const int qc = is_v ? item - kQuadChunks : item;
-        const int lq = qc >> 4;
-        const int lc = qc & 15;
+        for (int i = 0; i < 4; ++i) load_row(is_v, rs_k, rs_v, rr[i], lc, lreg[it][i]);
+      } else {
+        const int row0 = (tile - ntp) * kBN;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = row0 + lq * 4 + i;
-          if (is_v)
-            lreg[it][i] = load8<VDT, MV>(rc_v, row < L ? (row * kD + lc * 8) * kEV : -1);
-          else if constexpr (kSplit)
-            load8_split(rc_k, row < L ? (row * kD + lc * 8) * kEK : -1, lreg[it][i], lreg_lo[it][i]);
-          else
-            lreg[it][i] = load8<KDT, MQK>(rc_k, row < L ? (row * kD + lc * 8) * kEK : -1);
+          load_row(is_v, rc_k, rc_v, row < L ? row : -1, lc, lreg[it][i]);
         }
       }
     }
@@ -132,48 +223,44 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
       const int qc = is_v ? item - kQuadChunks : item;
       const int lq = qc >> 4;
       const int lc = qc & 15;
-      const u32x4_t* r = lreg[it];
+      const auto& r = lreg[it];
       if (!is_v) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          *reinterpret_cast<u32x4_t*>(k_lds + (lq * 4 + i) * kKPitch + lc * 16) = r[i];
-          if constexpr (kSplit)
-            *reinterpret_cast<u32x4_t*>(k_lds_lo + (lq * 4 + i) * kKPitch + lc * 16) = lreg_lo[it][i];
-        }
-      } else {
-        // transpose 4 keys x 8 d into 8 rows of V^T (4 keys each)
+        for (int p = 0; p < NQS; ++p)
 #pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-          u32x2_t even, odd;
-          even[0] = __builtin_amdgcn_perm(r[1][wi], r[0][wi], 0x05040100u);
-          even[1] = __builtin_amdgcn_perm(r[3][wi], r[2][wi], 0x05040100u);
-          odd[0] = __builtin_amdgcn_perm(r[1][wi], r[0][wi], 0x07060302u);
-          odd[1] = __builtin_amdgcn_perm(r[3][wi], r[2][wi], 0x07060302u);
-          uint8_t* row = vt_lds + (lc * 8 + 2 * wi) * kVtPitch + lq * 8;
-          *reinterpret_cast<u32x2_t*>(row) = even;
-          *reinterpret_cast<u32x2_t*>(row + kVtPitch) = odd;
-        }
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4_t*>(k_lds + p * kKBytes + (lq * 4 + i) * kKPitch + lc * 16) = r[i][p];
+      } else {
+        // transpose 4 keys x 8 d into 8 rows of V^T (4 keys each), per piece
+#pragma unroll
+        for (int p = 0; p < NVS; ++p)
+#pragma unroll
+          for (int wi = 0; wi < 4; ++wi) {
+            u32x2_t even, odd;
+            even[0] = __builtin_amdgcn_perm(r[1][p][wi], r[0][p][wi], 0x05040100u);
+            even[1] = __builtin_amdgcn_perm(r[3][p][wi], r[2][p][wi], 0x05040100u);
+            odd[0] = __builtin_amdgcn_perm(r[1][p][wi], r[0][p][wi], 0x07060302u);
+            odd[1] = __builtin_amdgcn_perm(r[3][p][wi], r[2][p][wi], 0x07060302u);
+            uint8_t* row = vt_lds + p * kVBytes + (lc * 8 + 2 * wi) * kVtPitch + lq * 8;
+            *reinterpret_cast<u32x2_t*>(row) = even;
+            *reinterpret_cast<u32x2_t*>(row + kVtPitch) = odd;
+          }
       }
     }
   };
 
   // Q fragments (B operand of S^T = K Q^T): query row, d = 16ks + 8g .. +7
   const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
-  u32x4_t qf[8];
-  u32x4_t qf_lo[kSplit ? 8 : 1];
+  u32x4_t qf[8][NQS];
   {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(
         static_cast<const uint8_t*>(a.q) + cur_row0 * kD * kEQ, static_cast<uint32_t>(L * kD * kEQ));
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int32_t off = qrow < L ? (qrow * kD + ks * 16 + g * 8) * kEQ : -1;
-      if constexpr (kSplit) {
-        load8_split(rq, off, qf[ks], qf_lo[ks]);
-        qf_lo[ks] ^= sc.q_sign;
-      } else {
-        qf[ks] = load8<QDT, MQK>(rq, off);
-      }
-      qf[ks] ^= sc.q_sign;
+      load8_pieces<QDT, MQK, NQS>(rq, off, qf[ks]);
+#pragma unroll
+      for (int p = 0; p < NQS; ++p) qf[ks][p] ^= sc.q_sign;
     }
   }
 
@@ -202,26 +289,35 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(k_lane + kb * 32 * kKPitch + ks * 32);
-        s[kb] = mfma32<MQK>(kf, qf[ks], s[kb]);
-        if constexpr (kSplit) {
-          const u32x4_t kl = *reinterpret_cast<const u32x4_t*>(k_lane + (k_lds_lo - k_lds) + kb * 32 * kKPitch + ks * 32);
-          s[kb] = mfma32<MQK>(kl, qf[ks], s[kb]);
-          s[kb] = mfma32<MQK>(kf, qf_lo[ks], s[kb]);
-        }
+        u32x4_t kf[NQS];
+#pragma unroll
+        for (int p = 0; p < NQS; ++p)
+          kf[p] = *reinterpret_cast<const u32x4_t*>(k_lane + p * kKBytes + kb * 32 * kKPitch + ks * 32);
+        s[kb] = mfma_split<MQK, NQS, NQS>(kf, qf[ks], s[kb]);
       }
     const int valid = t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN);
     softmax_tile(s, oacc, m_run, l_run, sc.c, sc.thresh, valid, g);
 #pragma unroll
     for (int u = 0; u < kBN / 16; ++u) {
-      const u32x4_t pf = p_operand<MV>(s, u);
+      u32x4_t pf[NPS];
+      {
+        const f32x16_t& sp = s[u >> 1];
+        const int j0 = 8 * (u & 1);
+        const float pv8[8] = {sp[j0 + 0], sp[j0 + 1], sp[j0 + 2], sp[j0 + 3],
+                              sp[j0 + 4], sp[j0 + 5], sp[j0 + 6], sp[j0 + 7]};
+        split8<MV, NPS>(pv8, pf);
+      }
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint8_t* row = v_lane + db * 32 * kVtPitch + 32 * u;
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 16);
-        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = mfma32<MV>(vf, pf, oacc[db]);
+        u32x4_t vf[NVS];
+#pragma unroll
+        for (int p = 0; p < NVS; ++p) {
+          const uint8_t* row = v_lane + p * kVBytes + db * 32 * kVtPitch + 32 * u;
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(row);
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(row + 16);
+          vf[p] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        }
+        oacc[db] = mfma_split<MV, NVS, NPS>(vf, pf, oacc[db]);
       }
     }
     __syncthreads();
@@ -229,24 +325,39 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_attn_staged_kernel(const AttnA
   write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
 }
 
-template <int QDT, int KDT, int VDT>
+template <int QDT, int KDT, int VDT, int NQS, int NPS, int NVS>
 hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
-  constexpr int NW = 8;
+  // The split modes hold more pieces in LDS and registers: one 4-wave
+  // workgroup per CU, so a wave may hold 512 registers (no spills).
+  constexpr bool kPlain = NQS <= 2 && NPS == 1 && NVS == 1;
+  constexpr int NW = kPlain ? 8 : 4;
+  constexpr int MINB = kPlain ? 2 : 1;
   const int32_t n_qt = (a.cur_len + NW * 32 - 1) / (NW * 32);
   const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  seg_attn_staged_kernel<QDT, KDT, VDT, NW><<<dim3(static_cast<uint32_t>(blocks)), NW * 64, 0, st>>>(
-      a, s, n_qt);
+  seg_attn_staged_kernel<QDT, KDT, VDT, NQS, NPS, NVS, NW, MINB>
+      <<<dim3(static_cast<uint32_t>(blocks)), NW * 64, 0, st>>>(a, s, n_qt);
   return hipGetLastError();
 }
 
-template <int QDT, int KDT>
+// Piece counts of the P V product for value type VDT.
+template <int QDT, int KDT, int VDT, int NQS>
+hipError_t dispatch_pv(const AttnArgs& a, const Scalars& s, hipStream_t st) {
+  if (a.value_dot_mode == kDotFp32) {
+    constexpr int nv = VDT == kBF16 ? 1 : (VDT == kF16 ? 2 : 3);
+    return launch<QDT, KDT, VDT, NQS, 3, nv>(a, s, st);
+  }
+  if constexpr (VDT == kF32) return launch<QDT, KDT, VDT, NQS, 2, 2>(a, s, st);
+  else return launch<QDT, KDT, VDT, NQS, 1, 1>(a, s, st);
+}
+
+template <int QDT, int KDT, int NQS>
 hipError_t dispatch_v(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   switch (a.v_dtype) {
-    case kBF16: return launch<QDT, KDT, kBF16>(a, s, st);
-    case kF16: return launch<QDT, KDT, kF16>(a, s, st);
-    case kF32: return launch<QDT, KDT, kF32>(a, s, st);
+    case kBF16: return dispatch_pv<QDT, KDT, kBF16, NQS>(a, s, st);
+    case kF16: return dispatch_pv<QDT, KDT, kF16, NQS>(a, s, st);
+    case kF32: return dispatch_pv<QDT, KDT, kF32, NQS>(a, s, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -256,9 +367,11 @@ hipError_t dispatch_v(const AttnArgs& a, const Scalars& s, hipStream_t st) {
 hipError_t launch_attention_staged(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream) {
   if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
   switch (a.q_dtype) {
-    case kBF16: return dispatch_v<kBF16, kBF16>(a, s, stream);
-    case kF16: return dispatch_v<kF16, kF16>(a, s, stream);
-    case kF32: return dispatch_v<kF32, kF32>(a, s, stream);
+    case kBF16: return dispatch_v<kBF16, kBF16, 1>(a, s, stream);
+    case kF16: return dispatch_v<kF16, kF16, 1>(a, s, stream);
+    case kF32:
+      return a.qk_dot_mode == kDotFp32 ? dispatch_v<kF32, kF32, 3>(a, s, stream)
+                                       : dispatch_v<kF32, kF32, 2>(a, s, stream);
     default: return hipErrorInvalidValue;
   }
 }

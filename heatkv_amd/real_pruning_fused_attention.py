@@ -16,14 +16,17 @@ Differences from the reference, all deliberate:
   is always the HIP kernel's.
 * Tile-shape knobs (``REAL_PRUNING_FUSED_BLOCK_M``/``_BLOCK_N``/
   ``_NUM_WARPS``/``_NUM_STAGES``) are read and validated like the
-  reference's but the kernel's tile shape is fixed by its MFMA layout.  The
-  dot-mode knobs are validated the same way (``ValueError`` on unknown
-  values); products always take 16-bit MFMA operands (bf16, or fp16 when the
-  inputs are fp16) with fp32 accumulation, which is the reference's default
-  ``bf16`` mode.  fp32 q and k (the cosine-attention model's, whose default
-  mode is a TF32 product) are split into bf16 high and low parts and
-  multiplied as hi*hi + hi*lo + lo*hi, about 16 significand bits; fp32 V and
-  the softmax weights enter the PV product rounded to bf16.
+  reference's but the kernel's tile shape is fixed by its MFMA layout.
+* The dot-mode knobs (``REAL_PRUNING_FUSED_QK_DOT_MODE`` bf16 / tf32 / fp32,
+  ``REAL_PRUNING_FUSED_VALUE_DOT_MODE`` bf16 / fp32) are validated like the
+  reference's and passed to the kernels, which meet or exceed each mode's
+  precision on 16-bit MFMAs with fp32 accumulation: 16-bit q/k products are
+  exact in every mode; fp32 q and k are split into 2 bf16 pieces (~16
+  significand bits, where the reference's bf16 / tf32 modes take a TF32
+  product) or, in the fp32 mode, 3 pieces (fp32's 24 bits).  P is rounded to
+  V's 16-bit type in the default value mode (fp32 V: P and V in 2 pieces,
+  where the reference takes a TF32 product); the fp32 value mode splits P in
+  3 pieces and V in as many as its type needs.
 """
 
 from __future__ import annotations
@@ -240,8 +243,8 @@ def fused_real_pruning_flat_segmented_attention(
     for knob, default in (("REAL_PRUNING_FUSED_BLOCK_M", 64), ("REAL_PRUNING_FUSED_BLOCK_N", 64),
                           ("REAL_PRUNING_FUSED_NUM_WARPS", 4), ("REAL_PRUNING_FUSED_NUM_STAGES", 3)):
         _positive_int_env(knob, default)
-    _fused_qk_dot_mode_id()
-    _fused_value_dot_mode_id()
+    qk_mode = _fused_qk_dot_mode_id()
+    value_mode = _fused_value_dot_mode_id()
 
     _lib.require_device(q.device)
     q = q.contiguous()
@@ -269,7 +272,7 @@ def fused_real_pruning_flat_segmented_attention(
         batch_size, num_heads, current_len,
         int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
         _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
-        _lib.dtype_code(out_dtype), float(softmax_scale), 1 if softmax_mode == "exp2" else 0,
+        _lib.dtype_code(out_dtype), float(softmax_scale), 1 if softmax_mode == "exp2" else 0, qk_mode, value_mode,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         stream.cuda_stream,
     )

@@ -89,6 +89,16 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *   use_exp2 : the reference's softmax_mode ("exp" = 0, "exp2" = 1); both give
  *              the same mathematical result and this kernel always evaluates
  *              exp2 with scale*log2(e) folded in.
+ *   qk_dot_mode : the reference's QK_DOT_MODE constexpr (:141-153, knob
+ *              REAL_PRUNING_FUSED_QK_DOT_MODE, :298-308): 0 bf16, 1 tf32,
+ *              2 fp32 (IEEE).  16-bit q/k products are exact in every mode;
+ *              fp32 q/k are split into 2 bf16 pieces in modes 0 and 1 (~16
+ *              significand bits, beyond TF32's 11) and 3 in mode 2 (fp32's 24).
+ *   value_dot_mode : the reference's VALUE_DOT_MODE (:176-184, knob
+ *              REAL_PRUNING_FUSED_VALUE_DOT_MODE, :286-295): 0 = P rounded to
+ *              V's type (fp32 V: P and V in 2 bf16 pieces, beyond the
+ *              reference's TF32 dot), 2 = an fp32 P V product (P in 3 pieces,
+ *              V in as many as its type needs).
  *   workspace, workspace_bytes : NULL / 0, or device memory of at least
  *              hkv_segmented_attention_workspace_bytes(device) bytes whose
  *              first 64 KiB (per-item counters) are zero before its first
@@ -113,6 +123,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int64_t slab_capacity, int32_t max_segments, int32_t head_dim,
                                 int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
                                 int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                int32_t qk_dot_mode, int32_t value_dot_mode,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

@@ -61,6 +61,7 @@ def flat_segmented_attention(
     dtype=np.float32,
     heads=None,
     batches=None,
+    workers=1,
 ):
     """Segmented attention over a flat slab + current keys.
 
@@ -71,7 +72,9 @@ def flat_segmented_attention(
     Returns ``(out [B, L, H*D], lse [B, H, L])`` in ``dtype`` (fp32 by default,
     fp64 when a tighter reference is wanted).  ``heads``/``batches`` restrict
     the work to a subset (the unlisted outputs are left NaN); used by the
-    bounded CPU-baseline sample.
+    bounded CPU-baseline sample.  ``workers > 1`` runs the (b, h) pairs on a
+    thread pool (numpy's matmul and exp release the GIL); every pair is the
+    same arithmetic either way, so the result does not depend on it.
     """
     q = np.asarray(q, dtype=dtype)
     cur_k = np.asarray(cur_k, dtype=dtype)
@@ -90,22 +93,31 @@ def flat_segmented_attention(
     scale = dtype(softmax_scale)
     head_list = range(H) if heads is None else heads
     batch_list = range(B) if batches is None else batches
+
+    def one(h, idx, b):
+        keys = np.concatenate([slab_k[b, idx, :].astype(dtype), cur_k[b, h]], axis=0)
+        vals = np.concatenate([slab_v[b, idx, :].astype(dtype), cur_v[b, h]], axis=0)
+        s = (q[b, h] @ keys.T) * scale  # [L, N]
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        l = p.sum(axis=1, keepdims=True)
+        o = (p @ vals) / l
+        out[b, :, h * D : (h + 1) * D] = o
+        lse[b, h, :] = (m + np.log(l))[:, 0]
+
+    pairs = []
     for h in head_list:
         _, idx = gather_head_keys(None, starts, ends, counts, h, 0)
-        for b in batch_list:
-            keys = np.concatenate(
-                [slab_k[b, idx, :].astype(dtype), cur_k[b, h]], axis=0
-            )
-            vals = np.concatenate(
-                [slab_v[b, idx, :].astype(dtype), cur_v[b, h]], axis=0
-            )
-            s = (q[b, h] @ keys.T) * scale  # [L, N]
-            m = s.max(axis=1, keepdims=True)
-            p = np.exp(s - m)
-            l = p.sum(axis=1, keepdims=True)
-            o = (p @ vals) / l
-            out[b, :, h * D : (h + 1) * D] = o
-            lse[b, h, :] = (m + np.log(l))[:, 0]
+        pairs.extend((h, idx, b) for b in batch_list)
+    if workers > 1 and len(pairs) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=int(workers)) as ex:
+            for f in [ex.submit(one, *p) for p in pairs]:
+                f.result()
+    else:
+        for p in pairs:
+            one(*p)
     return out, lse
 
 
@@ -145,3 +157,37 @@ def attention_flops(counts, starts, ends, batch, cur_len, head_dim):
         _, idx = gather_head_keys(None, starts, ends, counts, h, 0)
         total += 4 * cur_len * (len(idx) + cur_len) * head_dim
     return batch * total
+
+
+def flat_segmented_attention_sdpa(q, slab_k, slab_v, starts, ends, counts, cur_k, cur_v, softmax_scale):
+    """torch restatement of the reference CPU path, as it is written there.
+
+    ``_flat_segmented_attention_reference`` (real_pruning_fused_attention.py:
+    312-361): for every (b, h) gather head h's slab segments in table order
+    (entries with ``start >= end`` skipped), append the current K/V, and call
+    ``torch.nn.functional.scaled_dot_product_attention(..., scale=softmax_scale)``;
+    output ``[B, L, H * D]``.  Inputs are torch CPU tensors, computed in fp32
+    (the inputs are upcast first).  Used as the timed CPU baseline; pinned
+    against :func:`flat_segmented_attention` in tests/test_oracle_attention.py.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    q = q.float()
+    cur_k = cur_k.float()
+    cur_v = cur_v.float()
+    B, H, L, D = q.shape
+    if slab_k is None or slab_v is None:
+        slab_k = q.new_zeros((B, 0, D))
+        slab_v = q.new_zeros((B, 0, D))
+    slab_k = slab_k.float()
+    slab_v = slab_v.float()
+    out = q.new_empty((B, L, H * D))
+    for h in range(H):
+        _, idx = gather_head_keys(None, np.asarray(starts), np.asarray(ends), np.asarray(counts), h, 0)
+        index = torch.from_numpy(idx)
+        keys = torch.cat([slab_k.index_select(1, index), cur_k[:, h]], dim=1)  # [B, N, D]
+        vals = torch.cat([slab_v.index_select(1, index), cur_v[:, h]], dim=1)
+        o = F.scaled_dot_product_attention(q[:, h:h + 1], keys[:, None], vals[:, None], scale=softmax_scale)
+        out[:, :, h * D:(h + 1) * D] = o[:, 0]
+    return out

@@ -1,0 +1,114 @@
+"""The reference's dot-mode knobs change the arithmetic as they say.
+
+REAL_PRUNING_FUSED_QK_DOT_MODE (real_pruning_fused_attention.py:141-153,
+298-308) and REAL_PRUNING_FUSED_VALUE_DOT_MODE (:176-184, 286-295) select the
+precision of S = Q K^T and of O = P V.  Each mode is run through the operator
+on the GPU and compared with the fp64 oracle (oracle/segmented_attention.py)
+at bounds that only that mode's precision meets, next to the default mode's
+error on the same inputs:
+
+* QK fp32/ieee on fp32 q/k at cosine-attention scores of +-100: the LSE
+  (which does not involve the rounding of P) within 5e-5 (fp32 accumulation
+  of scores of that size); the default
+  2-piece split (~16 bits) is at least 4 times further off.
+* value fp32: the output within 2e-5 for bf16, fp16 and fp32 V; the default
+  mode rounds P to V's 16-bit type and is at least 10 times further off.
+* fp32 V in the default value mode: P and V carry ~16 bits (the reference
+  takes a TF32 dot there), output within 2e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from heatkv_amd import fused_real_pruning_flat_segmented_attention
+from oracle import segmented_attention as oattn
+from support import to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, dtype_qk, dtype_v, B=2, H=3, L=150, cap=500, S=5, cosine=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, H, L, 128), generator=g)
+    ck = torch.randn((B, H, L, 128), generator=g)
+    cv = torch.randn((B, H, L, 128), generator=g)
+    sk = torch.randn((B, cap, 128), generator=g)
+    sv = torch.randn((B, cap, 128), generator=g)
+    if cosine:
+        mul = torch.tensor([20.0, 55.0, 100.0][:H]).view(1, H, 1, 1)
+        q = torch.nn.functional.normalize(q, dim=-1) * mul
+        ck = torch.nn.functional.normalize(ck, dim=-1)
+        sk = torch.nn.functional.normalize(sk, dim=-1)
+    st = torch.zeros((H, S), dtype=torch.int32)
+    en = torch.zeros((H, S), dtype=torch.int32)
+    ct = torch.full((H,), S, dtype=torch.int32)
+    for h in range(H):
+        for i in range(S):
+            a = int(torch.randint(0, cap - 80, (1,), generator=g))
+            st[h, i] = a
+            en[h, i] = a + int(torch.randint(1, 80, (1,), generator=g))
+    return (q.to(dtype_qk), sk.to(dtype_qk), sv.to(dtype_v), (st, en, ct), ck.to(dtype_qk), cv.to(dtype_v))
+
+
+def _errors(case, scale, device, monkeypatch, qk_mode="bf16", value_mode="bf16"):
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", qk_mode)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_VALUE_DOT_MODE", value_mode)
+    q, sk, sv, (st, en, ct), ck, cv = case
+    out, lse = fused_real_pruning_flat_segmented_attention(
+        q=q.to(device), persisted_k=sk.to(device), persisted_v=sv.to(device), segment_starts=st.to(device),
+        segment_ends=en.to(device), segment_counts=ct.to(device), current_k=ck.to(device),
+        current_v=cv.to(device), softmax_scale=scale, return_lse=True, out_dtype=torch.float32)
+    torch.cuda.synchronize(device)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q).astype(np.float64), to_np(sk).astype(np.float64), to_np(sv).astype(np.float64),
+        st.numpy(), en.numpy(), ct.numpy(), to_np(ck).astype(np.float64), to_np(cv).astype(np.float64),
+        scale, dtype=np.float64)
+    o = out.double().cpu().numpy()
+    l = lse.double().cpu().numpy()
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    return float(np.abs(o - ref_out).max()), float(np.abs(l - ref_lse).max())
+
+
+@pytest.mark.parametrize("mode", ["fp32", "ieee"])
+def test_qk_fp32_mode_on_fp32_inputs(mode, device, monkeypatch):
+    print(f"[dot] QK {mode}, fp32 q/k, cosine scores", flush=True)
+    case = _case(81, torch.float32, torch.bfloat16, cosine=True)
+    _, lse_default = _errors(case, 1.0, device, monkeypatch)
+    _, lse_fp32 = _errors(case, 1.0, device, monkeypatch, qk_mode=mode)
+    print(f"[dot] LSE max-abs: default {lse_default:.3e}, {mode} {lse_fp32:.3e}", flush=True)
+    assert lse_fp32 <= 5e-5
+    assert lse_default >= 4 * lse_fp32
+
+
+@pytest.mark.parametrize("vdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_value_fp32_mode(vdt, device, monkeypatch):
+    print(f"[dot] value fp32, v={vdt}", flush=True)
+    case = _case(82, torch.bfloat16, vdt)
+    scale = 0.125
+    out_default, _ = _errors(case, scale, device, monkeypatch)
+    out_fp32, lse_fp32 = _errors(case, scale, device, monkeypatch, value_mode="fp32")
+    print(f"[dot] out max-abs: default {out_default:.3e}, fp32 {out_fp32:.3e}", flush=True)
+    assert out_fp32 <= 2e-5
+    assert lse_fp32 <= 2e-5
+    if vdt != torch.float32:  # fp32 V already gets a 2-piece P in the default mode
+        assert out_default >= 10 * out_fp32
+
+
+def test_fp32_v_default_mode_beyond_tf32(device, monkeypatch):
+    print("[dot] fp32 v, default value mode", flush=True)
+    case = _case(83, torch.bfloat16, torch.float32)
+    out_err, _ = _errors(case, 0.125, device, monkeypatch)
+    print(f"[dot] out max-abs {out_err:.3e}", flush=True)
+    assert out_err <= 2e-4
+
+
+def test_all_fp32_modes_together(device, monkeypatch):
+    """fp32 q, k and v with both knobs at fp32: every operand in 3 pieces."""
+    print("[dot] fp32 everything", flush=True)
+    case = _case(84, torch.float32, torch.float32, cosine=True)
+    out_err, lse_err = _errors(case, 1.0, device, monkeypatch, qk_mode="ieee", value_mode="fp32")
+    print(f"[dot] out max-abs {out_err:.3e} lse max-abs {lse_err:.3e}", flush=True)
+    assert out_err <= 1e-4 and lse_err <= 5e-5

@@ -365,7 +365,7 @@ def test_attention_output_not_16_byte_aligned(split, device, monkeypatch):
     code = _lib.load().hkv_segmented_attention(
         qd.data_ptr(), skd.data_ptr(), svd.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
         ckd.data_ptr(), cvd.data_ptr(), buf.data_ptr() + 8, None, B, H, L, cap, S, 128,
-        _lib.dtype_code(qd.dtype), _lib.dtype_code(ckd.dtype), _lib.dtype_code(cvd.dtype), 0, float(scale), 0,
+        _lib.dtype_code(qd.dtype), _lib.dtype_code(ckd.dtype), _lib.dtype_code(cvd.dtype), 0, float(scale), 0, 0, 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         stream.cuda_stream)
     _lib.check(code)

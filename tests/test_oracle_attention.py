@@ -178,3 +178,34 @@ def test_attention_flops_closed_form():
     ct = np.array([2, 1], np.int32)
     assert oattn.attention_flops(ct, st, en, batch=2, cur_len=10, head_dim=128) == \
         2 * (4 * 10 * (8 + 10) * 128 + 4 * 10 * (0 + 10) * 128)
+
+
+@pytest.mark.parametrize("seed", [4, 5])
+def test_thread_pool_gives_the_same_result(seed):
+    q, sk, sv, st, en, ct, ck, cv = _case(seed, B=3, H=4)
+    one = oattn.flat_segmented_attention(q, sk, sv, st, en, ct, ck, cv, 0.1)
+    many = oattn.flat_segmented_attention(q, sk, sv, st, en, ct, ck, cv, 0.1, workers=5)
+    assert np.array_equal(one[0], many[0]) and np.array_equal(one[1], many[1])
+
+
+@pytest.mark.parametrize("seed", [6, 7])
+def test_sdpa_restatement_matches_brute_force_and_numpy(seed):
+    """The torch restatement (timed as the CPU baseline) against the pure-Python
+    brute force on a small case and the numpy oracle on a larger one; a planted
+    mistake (current keys dropped) fails the comparison."""
+    q, sk, sv, st, en, ct, ck, cv = _case(seed, B=1, H=2, L=3, cap=12, S=3, D=8)
+    got = oattn.flat_segmented_attention_sdpa(*(torch.from_numpy(x) for x in (q, sk, sv)), st, en, ct,
+                                              torch.from_numpy(ck), torch.from_numpy(cv), 0.29).numpy()
+    D = q.shape[-1]
+    for h in range(2):
+        keys, vals = _gathered(q, sk, sv, st, en, ct, ck, cv, 0, h)
+        bo, _ = oattn.brute_force_attention(q[0, h].tolist(), keys.tolist(), vals.tolist(), 0.29)
+        np.testing.assert_allclose(got[0, :, h * D:(h + 1) * D], np.array(bo), rtol=1e-5, atol=1e-6)
+    q, sk, sv, st, en, ct, ck, cv = _case(seed, B=2, H=3, L=20, cap=80, S=5)
+    t = lambda x: torch.from_numpy(x)  # noqa: E731
+    got = oattn.flat_segmented_attention_sdpa(t(q), t(sk), t(sv), st, en, ct, t(ck), t(cv), 0.088).numpy()
+    ref, _ = oattn.flat_segmented_attention(q, sk, sv, st, en, ct, ck, cv, 0.088)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    bad = oattn.flat_segmented_attention_sdpa(t(q), t(sk), t(sv), st, en, ct, t(ck[:, :, :1]), t(cv[:, :, :1]),
+                                              0.088).numpy()
+    assert np.abs(bad - ref).max() > 1e-2
