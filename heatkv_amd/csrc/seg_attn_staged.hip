@@ -61,38 +61,50 @@ __device__ __forceinline__ void split8(const float (&v)[8], u32x4_t (&out)[NP]) 
   }
 }
 
-// 8 consecutive elements of type DT at byte offset `off` of `r` as NP
-// operand pieces (see split8); NP == 1 keeps the plain load8 conversion.
-// An offset of -1 yields zeros.
+// 8 consecutive elements of type DT, as loaded: 32 bytes for fp32, 16 for
+// 16-bit types (w[1] unused).
+struct Raw8 {
+  u32x4_t w[2];
+};
+
+// Raw load of 8 elements of type DT at byte offset `off` of `r` (an offset of
+// -1 yields zeros).
+template <int DT>
+__device__ __forceinline__ Raw8 load_raw8(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  Raw8 x;
+  x.w[0] = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  if constexpr (DT == kF32) x.w[1] = __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0);
+  else x.w[1] = u32x4_t{};
+  return x;
+}
+
+// The 8 raw elements as NP operand pieces (see split8); NP == 1 with a
+// 16-bit DT equal to MT is the raw data itself.
 template <int DT, int MT, int NP>
-__device__ __forceinline__ void load8_pieces(__amdgpu_buffer_rsrc_t r, int32_t off, u32x4_t (&out)[NP]) {
-  if constexpr (NP == 1) {
-    out[0] = load8<DT, MT>(r, off);
+__device__ __forceinline__ void pieces8(const Raw8& x, u32x4_t (&out)[NP]) {
+  if constexpr (NP == 1 && DT == MT) {
+    out[0] = x.w[0];
   } else {
+    // Whole-vector bit casts first: extracting single elements of a buffer
+    // load's result and casting them miscompiles with this toolchain (the
+    // vector load becomes one dword load, replicated).
+    const f32x4_t x0 = __builtin_bit_cast(f32x4_t, x.w[0]);
+    const f32x4_t x1 = __builtin_bit_cast(f32x4_t, x.w[1]);
     float v[8];
-    if constexpr (DT == kF32) {
-      const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-      const f32x4_t y = __builtin_bit_cast(
-          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off < 0 ? -1 : off + 16, 0, 0));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = x[i];
-        v[4 + i] = y[i];
-      }
-    } else {
-      const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if constexpr (DT == kF16) {
-          v[2 * i] = f16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-          v[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(w[i] >> 16));
-        } else {
-          v[2 * i] = __builtin_bit_cast(float, w[i] << 16);
-          v[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
-        }
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == kF32) {
+        v[i] = x0[i];
+        v[4 + i] = x1[i];
+      } else if constexpr (DT == kF16) {
+        v[2 * i] = f16_to_f32(static_cast<uint16_t>(x.w[0][i] & 0xffffu));
+        v[2 * i + 1] = f16_to_f32(static_cast<uint16_t>(x.w[0][i] >> 16));
+      } else {
+        v[2 * i] = __builtin_bit_cast(float, x.w[0][i] << 16);
+        v[2 * i + 1] = __builtin_bit_cast(float, x.w[0][i] & 0xffff0000u);
       }
     }
-    split8<kBF16, NP>(v, out);
+    split8<MT, NP>(v, out);
   }
 }
 
@@ -133,7 +145,6 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   constexpr int kEQ = QDT == kF32 ? 4 : 2;
   constexpr int kKBytes = kBN * kKPitch;
   constexpr int kVBytes = kD * kVtPitch;
-  constexpr int kNL = NQS > NVS ? NQS : NVS;  // pieces held per staged load
   static_assert(2 * kQuadChunks % kThreads == 0, "loader split");
   static_assert(NQS >= 1 && NQS <= 3 && NPS >= 1 && NPS <= 3 && NVS >= 1 && NVS <= 3, "pieces");
 
@@ -177,20 +188,12 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   int cur_seg = 0;
   // quad-chunk i covers keys 4(i/16)..+3 at d 8(i%16)..+7 of K (i < kQuadChunks)
   // or of V; thread tid owns quad-chunks tid, tid + kThreads, ...
-  u32x4_t lreg[kLoadsPerThread][4][kNL];
+  // raw elements in flight, split into operand pieces when stored to LDS
+  Raw8 lreg[kLoadsPerThread][4];
   auto load_row = [&](bool is_v, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int32_t row, int lc,
-                      u32x4_t (&dst)[kNL]) {
-    if (is_v) {
-      u32x4_t p[NVS];
-      load8_pieces<VDT, MV, NVS>(rv, row < 0 ? -1 : (row * kD + lc * 8) * kEV, p);
-#pragma unroll
-      for (int i = 0; i < NVS; ++i) dst[i] = p[i];
-    } else {
-      u32x4_t p[NQS];
-      load8_pieces<KDT, MQK, NQS>(rk, row < 0 ? -1 : (row * kD + lc * 8) * kEK, p);
-#pragma unroll
-      for (int i = 0; i < NQS; ++i) dst[i] = p[i];
-    }
+                      Raw8& dst) {
+    if (is_v) dst = load_raw8<VDT>(rv, row < 0 ? -1 : (row * kD + lc * 8) * kEV);
+    else dst = load_raw8<KDT>(rk, row < 0 ? -1 : (row * kD + lc * 8) * kEK);
   };
   auto issue_loads = [&](int tile, int buf) {
 #pragma unroll
@@ -223,14 +226,19 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
       const int qc = is_v ? item - kQuadChunks : item;
       const int lq = qc >> 4;
       const int lc = qc & 15;
-      const auto& r = lreg[it];
       if (!is_v) {
 #pragma unroll
-        for (int p = 0; p < NQS; ++p)
+        for (int i = 0; i < 4; ++i) {
+          u32x4_t pc[NQS];
+          pieces8<KDT, MQK, NQS>(lreg[it][i], pc);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4_t*>(k_lds + p * kKBytes + (lq * 4 + i) * kKPitch + lc * 16) = r[i][p];
+          for (int p = 0; p < NQS; ++p)
+            *reinterpret_cast<u32x4_t*>(k_lds + p * kKBytes + (lq * 4 + i) * kKPitch + lc * 16) = pc[p];
+        }
       } else {
+        u32x4_t r[4][NVS];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pieces8<VDT, MV, NVS>(lreg[it][i], r[i]);
         // transpose 4 keys x 8 d into 8 rows of V^T (4 keys each), per piece
 #pragma unroll
         for (int p = 0; p < NVS; ++p)
@@ -258,7 +266,7 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int32_t off = qrow < L ? (qrow * kD + ks * 16 + g * 8) * kEQ : -1;
-      load8_pieces<QDT, MQK, NQS>(rq, off, qf[ks]);
+      pieces8<QDT, MQK, NQS>(load_raw8<QDT>(rq, off), qf[ks]);
 #pragma unroll
       for (int p = 0; p < NQS; ++p) qf[ks][p] ^= sc.q_sign;
     }

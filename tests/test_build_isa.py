@@ -55,3 +55,13 @@ def test_m0_only_inside_inline_asm(src, tmp_path):
 def test_no_scratch_spills(src, tmp_path):
     text = _asm(src, tmp_path)
     assert "scratch_store" not in text and "scratch_load" not in text
+
+
+@pytest.mark.parametrize("src", ["seg_attn_direct.hip", "seg_attn_staged.hip"])
+def test_operand_loads_stay_16_byte_vectors(src, tmp_path):
+    """Every buffer load of the attention kernels moves 16 bytes per lane.  A
+    single-dword buffer load here is the toolchain's miscompile of a 16-byte
+    load whose elements are extracted and cast one by one (one dword loaded
+    and replicated), which corrupts fp32 q / k / v."""
+    text = _asm(src, tmp_path)
+    assert not re.search(r"\bbuffer_load_dword\b", text)
