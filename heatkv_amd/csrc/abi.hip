@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/heatkv.h"
@@ -37,6 +38,41 @@ int32_t elem_bytes(int32_t dt) {
     case HKV_DTYPE_F32: return 4;
     default: return 0;
   }
+}
+
+// ------------------------------------------------ allocation-free attention
+//
+// Workspace of hkv_segmented_attention_noalloc: the round split's counters
+// plus two partial records per resident workgroup slot, for up to
+// kScratchSlots slots (a 256-CU device at 2 workgroups per CU): 69.3 MB in
+// every GPU the library runs on, held until the process ends.  Host code
+// never uses the array's name as an address: each device's copy is looked up
+// once with hipGetSymbolAddress and that pointer is what the kernels get.
+constexpr int32_t kScratchSlots = 512;
+constexpr int64_t kScratchBytes =
+    hkv::kCounterBytes + 2LL * kScratchSlots * hkv::kPartialFloats * static_cast<int64_t>(sizeof(float));
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+__global__ void clear_words(uint32_t* p, int32_t n) {
+  for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// This device's scratch (device current), its counters cleared on `stream`
+// at the first call; null when the runtime cannot give its address.
+void* device_scratch(int device, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device] != nullptr) return g_scratch[device];
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+  // the kernels leave the counters zero after every call; they start zero here
+  clear_words<<<16, 256, 0, stream>>>(static_cast<uint32_t*>(ptr), static_cast<int32_t>(hkv::kCounterBytes / 4));
+  if (hipGetLastError() != hipSuccess) return nullptr;
+  g_scratch[device] = ptr;
+  return ptr;
 }
 
 }  // namespace
@@ -254,6 +290,36 @@ int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bi
   const hipError_t e = hkv::launch_produce(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(HKV_ERR_LAUNCH, "qkv producer launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const void* slab_v,
+                                        const int32_t* seg_starts, const int32_t* seg_ends,
+                                        const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                        void* out, float* lse, int32_t batch, int32_t heads,
+                                        int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                        int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                        int32_t v_dtype, int32_t out_dtype, float softmax_scale,
+                                        int32_t use_exp2, int32_t qk_dot_mode, int32_t value_dot_mode,
+                                        void* stream) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
+  if (device < 0 || device >= kMaxDevices)
+    return fail(HKV_ERR_UNSUPPORTED, "device %d: the allocation-free entry point serves devices 0..%d", device,
+                kMaxDevices - 1);
+  const int32_t slots = hkv::split_slots(device);
+  if (slots <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
+  const int64_t need = hkv::split_workspace_bytes(slots);
+  if (need > kScratchBytes)
+    return fail(HKV_ERR_UNSUPPORTED,
+                "device %d has %d resident workgroup slots; the allocation-free entry point's workspace "
+                "(%lld bytes) serves at most %d",
+                device, slots, static_cast<long long>(kScratchBytes), kScratchSlots);
+  void* ws = device_scratch(device, static_cast<hipStream_t>(stream));
+  if (ws == nullptr) return fail(HKV_ERR_DEVICE, "cannot resolve the attention scratch on device %d", device);
+  return hkv_segmented_attention(q, slab_k, slab_v, seg_starts, seg_ends, seg_counts, cur_k, cur_v, out, lse,
+                                 batch, heads, cur_len, slab_capacity, max_segments, head_dim, q_dtype, k_dtype,
+                                 v_dtype, out_dtype, softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, ws,
+                                 kScratchBytes, stream);
 }
 
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device) {

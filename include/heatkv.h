@@ -135,6 +135,30 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device);
 
 /*
+ * hkv_segmented_attention with its workspace taken from a static device
+ * array of this library instead of the caller: the entry point allocates
+ * nothing (no hipMalloc, hipFree or allocating library routine), for callers
+ * that cannot allocate -- code under HIP graph capture, serving loops and
+ * harnesses that forbid allocation.  No counterpart in the reference.
+ * Arguments and results as hkv_segmented_attention (the workspace arguments
+ * are absent).  The array holds the round split's counters and partial
+ * records for up to 512 resident workgroup slots (a 256-CU device): 69.3 MB
+ * per GPU the library runs on, held until the process ends; a device with
+ * more slots is rejected (HKV_ERR_UNSUPPORTED).  Every call on one GPU shares
+ * that GPU's array, so calls that may overlap on one GPU (other streams,
+ * other host threads) race; calls in order on one stream do not.
+ */
+int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const void* slab_v,
+                                        const int32_t* seg_starts, const int32_t* seg_ends,
+                                        const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                        void* out, float* lse, int32_t batch, int32_t heads,
+                                        int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                        int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                        int32_t v_dtype, int32_t out_dtype, float softmax_scale,
+                                        int32_t use_exp2, int32_t qk_dot_mode, int32_t value_dot_mode,
+                                        void* stream);
+
+/*
  * QKV producer epilogue of one scale: from the QKV projection output to the
  * attention-ready q, k, v, for every (b, l, h):
  *   x_q, x_k, x_v = qkv[b, l, 0|1|2, h, :] (+ q_bias / v_bias[h*D:(h+1)*D])
