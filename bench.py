@@ -112,14 +112,20 @@ def parse():
 
 
 def attention_call(wl, device):
-    """Inputs of one final-step call on ``device`` (slab packed by the HIP pack kernel)."""
+    """Inputs of one final-step call on ``device`` (slab packed by the HIP pack
+    kernel), with the work plan of its tables (built on the host once, as the
+    segmented cache does per layer and target; HKV_ATTN_PLAN=0 leaves it out)."""
     from heatkv_amd import workloads as W
+    from heatkv_amd.segmented_cache import work_plans_enabled
 
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
+    plan = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len)
+            if work_plans_enabled(device) else None)
     return dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
-                segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale)
+                segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale,
+                work_plan=plan)
 
 
 def clock_ramp(fn, device, min_ms=300.0, max_wall_s=5.0, chunk=50):

@@ -9,6 +9,7 @@ descriptors) is computed on the host like the reference's.
 from .real_pruning_fused_attention import (  # noqa: F401
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
+    segmented_attention_plan,
 )
 from .slab_schedule import (  # noqa: F401
     SIDES_1M,

@@ -52,14 +52,17 @@ SIGNATURES = {
         _c_i32,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
          _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
-         _c_i32, _c_p, _c_i64, _c_p],
+         _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p],
     ),
     "hkv_segmented_attention_noalloc": (
         _c_i32,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
          _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
-         _c_i32, _c_p],
+         _c_i32, _c_p, _c_i32, _c_p],
     ),
+    "hkv_segmented_attention_plan": (
+        _c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i32]),
+    "hkv_segmented_attention_slots": (_c_i32, [_c_i32]),
     "hkv_segmented_attention_workspace_bytes": (_c_i64, [_c_i32]),
     "hkv_qkv_produce": (
         _c_i32,

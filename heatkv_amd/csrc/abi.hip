@@ -148,12 +148,15 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
                                 int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
                                 int32_t qk_dot_mode, int32_t value_dot_mode,
+                                const int32_t* work_plan, int32_t plan_units,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (qk_dot_mode < 0 || qk_dot_mode > 2)
     return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
   if (value_dot_mode != 0 && value_dot_mode != 2)
     return fail(HKV_ERR_INVALID_ARG, "value_dot_mode must be 0 (bf16) or 2 (fp32) (got %d)", value_dot_mode);
+  if (work_plan != nullptr && plan_units < 0)
+    return fail(HKV_ERR_INVALID_ARG, "plan_units must be >= 0 (got %d)", plan_units);
   if (head_dim != 128)
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented v1 only supports head_dim=128");
   if (cur_len <= 0)
@@ -226,6 +229,8 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   a.value_dot_mode = value_dot_mode;
   a.workspace = workspace;
   a.workspace_bytes = workspace != nullptr ? workspace_bytes : 0;
+  a.plan = work_plan;
+  a.plan_units = work_plan != nullptr ? plan_units : 0;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));
@@ -300,7 +305,7 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
                                         int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
                                         int32_t v_dtype, int32_t out_dtype, float softmax_scale,
                                         int32_t use_exp2, int32_t qk_dot_mode, int32_t value_dot_mode,
-                                        void* stream) {
+                                        const int32_t* work_plan, int32_t plan_units, void* stream) {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
   if (device < 0 || device >= kMaxDevices)
@@ -318,8 +323,37 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
   if (ws == nullptr) return fail(HKV_ERR_DEVICE, "cannot resolve the attention scratch on device %d", device);
   return hkv_segmented_attention(q, slab_k, slab_v, seg_starts, seg_ends, seg_counts, cur_k, cur_v, out, lse,
                                  batch, heads, cur_len, slab_capacity, max_segments, head_dim, q_dtype, k_dtype,
-                                 v_dtype, out_dtype, softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, ws,
-                                 kScratchBytes, stream);
+                                 v_dtype, out_dtype, softmax_scale, use_exp2, qk_dot_mode, value_dot_mode,
+                                 work_plan, plan_units, ws, kScratchBytes, stream);
+}
+
+int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
+                                     const int32_t* seg_counts, int32_t heads, int32_t max_segments,
+                                     int64_t slab_capacity, int32_t batch, int32_t cur_len, int32_t slots,
+                                     int32_t* units, int32_t max_units) {
+  if (heads <= 0 || heads > 1024 || batch <= 0 || cur_len <= 0)
+    return fail(HKV_ERR_INVALID_ARG, "heads in [1, 1024], batch and cur_len positive (got %d, %d, %d)", heads, batch,
+                cur_len);
+  if (max_segments < 0 || max_segments > hkv::kMaxSegments)
+    return fail(HKV_ERR_UNSUPPORTED, "max_segments must be in [0, %d] (got %d)", hkv::kMaxSegments, max_segments);
+  if (slab_capacity < 0 || slots < 0 || max_units < 0)
+    return fail(HKV_ERR_INVALID_ARG, "slab_capacity, slots and max_units must be >= 0");
+  if (!seg_counts || (max_segments > 0 && (!seg_starts || !seg_ends)))
+    return fail(HKV_ERR_INVALID_ARG, "null table pointer");
+  const int64_t items = static_cast<int64_t>(batch) * heads * ((cur_len + 127) / 128);
+  if (items > 0x3fffffffLL / 2) return fail(HKV_ERR_UNSUPPORTED, "too many work items (%lld)", static_cast<long long>(items));
+  const int32_t n = hkv::build_attention_plan(seg_starts, seg_ends, seg_counts, heads, max_segments, slab_capacity,
+                                              batch, cur_len, slots, units, max_units);
+  if (n < 0) return fail(HKV_ERR_INVALID_ARG, "the plan needs more than max_units = %d units", max_units);
+  ok();
+  return n;
+}
+
+int32_t hkv_segmented_attention_slots(int32_t device) {
+  const int32_t s = hkv::split_slots(device);
+  if (s <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
+  ok();
+  return s;
 }
 
 int64_t hkv_segmented_attention_workspace_bytes(int32_t device) {

@@ -61,7 +61,17 @@ struct AttnArgs {
   int32_t value_dot_mode;   // DotMode of O = P V (kDotTf32 not used)
   void* workspace;          // round-split storage, or null
   int64_t workspace_bytes;
+  const int32_t* plan;      // work plan (kPlanInts ints per unit), or null: planned in the kernel
+  int32_t plan_units;
+  int32_t ws_cuts;          // cut items the workspace holds (set by the launch)
 };
+
+// Work plan units (build_attention_plan): head, index in the head
+// (b * n_qt + qt), key tiles [t0, t1), cut item (-1 = whole) and part.
+constexpr int kPlanInts = 8;
+int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
+                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t slots,
+                             int32_t* out, int32_t max_units);
 
 constexpr int kMaxSegments = 256;
 

@@ -1,0 +1,191 @@
+// Host-side work plan of the 16-bit segmented-attention kernel.
+//
+// Without a plan every workgroup of the kernel computes the launch's work
+// order from the device offset tables itself (heaviest head first, and the
+// round split), a few microseconds per workgroup.  The tables of a (layer,
+// target) do not change during a generation, so the caller can build the
+// order once on the host from its copy of the tables and pass it with every
+// call (as the reference uploads its offset tables once per layer and target,
+// enable_real_pruning_fast.py:592-608).  A plan is a list of units, one per
+// workgroup in dispatch order: a whole item (b, h, 128-query tile) or one of
+// the two key-range parts of a cut item.
+//
+// Choosing the cuts.  The hardware dispatches workgroups in id order to
+// whatever slot frees first, i.e. list scheduling.  The plan simulates it
+// over the device's resident slots (2 per CU) with a per-unit cost of its key
+// tiles plus a fixed overhead (a part pays more: it publishes and merges a
+// partial record), for cutting the k heaviest items at a fraction f of their
+// tiles, whole items first (heaviest first), then the parts (longest first),
+// and keeps the (k, f) with the shortest simulated makespan.  Launches with
+// many rounds of items per slot balance without cuts and are not searched.
+#include <algorithm>
+#include <functional>
+#include <queue>
+#include <vector>
+
+#include "hkv_internal.h"
+
+namespace hkv {
+namespace {
+
+constexpr int kPlanBN = 64;            // keys per tile
+constexpr int kPlanBM = 128;           // queries per item
+constexpr int kPlanMinPartTiles = 8;   // a part must have this many key tiles
+constexpr double kUnitOverTiles = 1.5;  // start-up of a workgroup, in key-tile times
+constexpr double kPartOverTiles = 4.0;  // record publish + merge of a part
+constexpr int kNoSearchRounds = 4;     // items per slot above which nothing is cut
+
+struct Item {
+  int32_t h, j, n;
+};
+
+double simulate(const std::vector<std::pair<int32_t, bool>>& units, int slots) {
+  std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+  for (int s = 0; s < slots; ++s) free_at.push(0.0);
+  double end = 0.0;
+  for (const auto& u : units) {
+    const double t = free_at.top();
+    free_at.pop();
+    const double f = t + u.first + kUnitOverTiles + (u.second ? kPartOverTiles : 0.0);
+    end = std::max(end, f);
+    free_at.push(f);
+  }
+  return end;
+}
+
+struct Cut {
+  int32_t k = 0;   // heaviest items cut
+  double f = 0.5;  // fraction of an item's tiles in its first part
+};
+
+int32_t first_part(int32_t n, double f) {
+  int32_t a = static_cast<int32_t>(n * f + 0.5);
+  return std::min(std::max(a, kPlanMinPartTiles), n - kPlanMinPartTiles);
+}
+
+bool cuttable(int32_t n) { return n >= 2 * kPlanMinPartTiles; }
+
+std::vector<std::pair<int32_t, bool>> units_for(const std::vector<Item>& items, const Cut& c) {
+  std::vector<std::pair<int32_t, bool>> whole, parts;
+  for (size_t i = 0; i < items.size(); ++i) {
+    const int32_t n = items[i].n;
+    if (static_cast<int32_t>(i) < c.k && cuttable(n)) {
+      const int32_t a = first_part(n, c.f);
+      parts.push_back({a, true});
+      parts.push_back({n - a, true});
+    } else {
+      whole.push_back({n, false});
+    }
+  }
+  std::stable_sort(parts.begin(), parts.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
+  whole.insert(whole.end(), parts.begin(), parts.end());
+  return whole;
+}
+
+// Workgroup j's item when every item is whole: the 8 XCDs take workgroup ids
+// round robin (j % 8), so with at least 8 (head, batch row) groups per XCD the
+// query tiles of one group are dealt to one XCD (groups snake over the XCDs),
+// sharing its L2.  Identity otherwise.
+int32_t xcd_order(int32_t j, int32_t groups, int32_t n_qt) {
+  constexpr int kXcds = 8;
+  if (groups % kXcds != 0 || groups < 8 * kXcds) return j;
+  const int32_t x = j % kXcds;
+  const int32_t k = j / kXcds;
+  const int32_t lg = k / n_qt;
+  const int32_t qt = k - lg * n_qt;
+  const int32_t group = lg * kXcds + ((lg & 1) ? kXcds - 1 - x : x);
+  return group * n_qt + qt;
+}
+
+}  // namespace
+
+int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
+                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t slots,
+                             int32_t* out, int32_t max_units) {
+  const int32_t n_qt = (L + kPlanBM - 1) / kPlanBM;
+  const int32_t ntc = (L + kPlanBN - 1) / kPlanBN;
+  std::vector<int64_t> rows(H, 0);
+  for (int32_t h = 0; h < H; ++h) {
+    int32_t n = seg_counts[h];
+    n = n < 0 ? 0 : (n > S ? S : n);
+    for (int32_t i = 0; i < n; ++i) {
+      int64_t st = seg_starts[static_cast<int64_t>(h) * S + i];
+      int64_t en = seg_ends[static_cast<int64_t>(h) * S + i];
+      st = st < 0 ? 0 : (st > cap ? cap : st);
+      en = en < 0 ? 0 : (en > cap ? cap : en);
+      rows[h] += en > st ? en - st : 0;
+    }
+  }
+  // heads heaviest first (ties by index); within a head its items in order
+  std::vector<int32_t> heads(H);
+  for (int32_t h = 0; h < H; ++h) heads[h] = h;
+  std::stable_sort(heads.begin(), heads.end(), [&](int32_t x, int32_t y) { return rows[x] > rows[y]; });
+  const int32_t per_h = B * n_qt;
+  std::vector<Item> items;
+  items.reserve(static_cast<size_t>(H) * per_h);
+  for (int32_t h : heads) {
+    const int32_t n = static_cast<int32_t>((rows[h] + kPlanBN - 1) / kPlanBN) + ntc;
+    for (int32_t j = 0; j < per_h; ++j) items.push_back({h, j, n});
+  }
+  const int32_t N = static_cast<int32_t>(items.size());
+
+  Cut best;
+  const bool any_cuttable = std::any_of(items.begin(), items.end(), [](const Item& it) { return cuttable(it.n); });
+  if (slots > 0 && N < kNoSearchRounds * slots && any_cuttable) {
+    double best_t = simulate(units_for(items, best), slots);
+    const int32_t kmax = std::min(N, slots);  // one counter and two records per cut item
+    const int32_t step = std::max(1, slots / 32);
+    for (int32_t k = step; k <= kmax; k += step) {
+      for (double f : {0.5, 0.6, 0.7}) {
+        const Cut c{k, f};
+        const double t = simulate(units_for(items, c), slots);
+        if (t < best_t * 0.995) {
+          best_t = t;
+          best = c;
+        }
+      }
+    }
+  }
+
+  // emit: whole items, then the parts of cut items (longest first)
+  struct Unit {
+    int32_t h, j, t0, t1, cut, part;
+  };
+  std::vector<Unit> whole, parts;
+  int32_t cuts = 0;
+  for (int32_t i = 0; i < N; ++i) {
+    const Item& it = items[i];
+    if (i < best.k && cuttable(it.n)) {
+      const int32_t a = first_part(it.n, best.f);
+      parts.push_back({it.h, it.j, 0, a, cuts, 0});
+      parts.push_back({it.h, it.j, a, it.n, cuts, 1});
+      ++cuts;
+    } else {
+      whole.push_back({it.h, it.j, 0, it.n, -1, 0});
+    }
+  }
+  std::stable_sort(parts.begin(), parts.end(),
+                   [](const Unit& x, const Unit& y) { return x.t1 - x.t0 > y.t1 - y.t0; });
+  const int32_t n_units = static_cast<int32_t>(whole.size() + parts.size());
+  if (out == nullptr) return n_units;
+  if (n_units > max_units) return -1;
+  const bool grouped = parts.empty();
+  int32_t u = 0;
+  auto emit = [&](const Unit& x) {
+    int32_t* o = out + static_cast<int64_t>(u++) * kPlanInts;
+    o[0] = x.h;
+    o[1] = x.j;
+    o[2] = x.t0;
+    o[3] = x.t1;
+    o[4] = x.cut;
+    o[5] = x.part;
+    o[6] = 0;
+    o[7] = 0;
+  };
+  for (int32_t k = 0; k < static_cast<int32_t>(whole.size()); ++k)
+    emit(whole[grouped ? xcd_order(k, H * B, n_qt) : k]);
+  for (const Unit& x : parts) emit(x);
+  return n_units;
+}
+
+}  // namespace hkv

@@ -205,26 +205,67 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
   const int g = lane >> 5;
 
-  Unit un = split_unit(split, static_cast<int32_t>(blockIdx.x));
-  if (split.two == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
-  int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
-  const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
-                                         a.max_segments, a.batch, n_qt, head_rows,
-                                         head_rows + kMaxHeads, seg_start, seg_pref, un.item,
-                                         head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
+  Unit un;
+  WorkItem w;
+  int32_t t_begin, t_end, parts;
+  const int32_t ntc = (L + kBN - 1) / kBN;
+  if (a.plan != nullptr) {
+    // the unit of this workgroup from the caller's work plan
+    const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
+    const int32_t ph = pu[0], pj = pu[1], p0 = pu[2], p1 = pu[3], pcut = pu[4], ppart = pu[5];
+    if (ph < 0 || ph >= H || pj < 0 || pj >= a.batch * n_qt) return;  // not a unit of this launch
+    w.h = ph;
+    w.b = pj / n_qt;
+    w.qt = pj - w.b * n_qt;
+    w.bh = w.b * H + w.h;
+    load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
+                                 seg_pref);
+    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
+    t_begin = p0 < 0 ? 0 : (p0 > ntiles ? ntiles : p0);
+    t_end = p1 < t_begin ? t_begin : (p1 > ntiles ? ntiles : p1);
+    // a cut item's record and counter exist when the launch has a workspace
+    const bool cut = pcut >= 0 && a.workspace != nullptr && pcut < a.ws_cuts && ppart >= 0 &&
+                     ppart < 2;
+    parts = cut ? 2 : 1;
+    un.item = 0;
+    un.part = cut ? ppart : 0;
+    un.parts = parts;
+    un.record = cut ? 2 * pcut : 0;
+    un.counter = cut ? pcut : 0;
+    if (!cut) {  // a whole item, whatever the plan's range says
+      t_begin = 0;
+      t_end = ntiles;
+    }
+    if (t_begin >= t_end && !cut) return;
+  } else {
+    un = split_unit(split, static_cast<int32_t>(blockIdx.x));
+    if (split.two == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
+    int32_t* head_rows = reinterpret_cast<int32_t*>(ring);
+    w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H, a.max_segments, a.batch, n_qt,
+                            head_rows, head_rows + kMaxHeads, seg_start, seg_pref, un.item,
+                            head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
+    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
+    // A part needs kMinPartTiles key tiles to pay for its record and the
+    // merge, so a short item runs as fewer parts (one, below two such runs);
+    // every part of the item sees the same tile count and agrees.  Parts past
+    // the count leave at once.
+    parts = ntiles / kMinPartTiles;
+    parts = parts < 1 ? 1 : (parts < un.parts ? parts : un.parts);
+    if (un.part >= parts) return;
+    t_begin = un.part * ntiles / parts;
+    t_end = (un.part + 1) * ntiles / parts;
+  }
   const int32_t R = w.R;
   const int32_t ntp = (R + kBN - 1) / kBN;
-  const int32_t ntc = (L + kBN - 1) / kBN;
-  const int32_t ntiles = ntp + ntc;
-  // A part needs kMinPartTiles key tiles to pay for its record and the
-  // merge, so a short item runs as fewer parts (one, below two such runs);
-  // every part of the item sees the same tile count and agrees.  Parts past
-  // the count leave at once.
-  int32_t parts = ntiles / kMinPartTiles;
-  parts = parts < 1 ? 1 : (parts < un.parts ? parts : un.parts);
-  if (un.part >= parts) return;
-  const int32_t t_begin = un.part * ntiles / parts;
-  const int32_t t_end = (un.part + 1) * ntiles / parts;
+  if (t_begin >= t_end) {
+    // a planned part with no key tiles (a plan that does not match these
+    // tables): its record is empty -- zero weight in the merge
+    const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
+    f32x16_t none[4] = {};
+    merge_parts<QDT, kThreads>(a, sc, un, parts, none, -1e30f, 0.f, w, qrow, L, H, g, merge_turn,
+                               ring + wave * 32 * kOutPitch);
+    return;
+  }
 
   const bool k_wave = wave * kDmaPerWave < 16;
   const int64_t cur_row0 = static_cast<int64_t>(w.bh) * L;
@@ -438,8 +479,19 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   RoundSplit split{static_cast<int32_t>(items), 0, 0, 0};
   if (slots > 0 && a.workspace_bytes >= split_workspace_bytes(slots))
     split = round_split(static_cast<int32_t>(items), slots, (a.cur_len + kBN - 1) / kBN);
+  AttnArgs b = a;
+  b.ws_cuts = 0;
+  if (a.workspace != nullptr && a.workspace_bytes > kCounterBytes) {
+    const int64_t by_records = (a.workspace_bytes - kCounterBytes) / (2LL * kPartialFloats * 4);
+    b.ws_cuts = static_cast<int32_t>(by_records < kCounterBytes / 4 ? by_records : kCounterBytes / 4);
+  }
+  if (a.plan != nullptr) {
+    if (a.plan_units <= 0) return hipSuccess;
+    seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(a.plan_units)), 256, 0, st>>>(b, s, n_qt, split);
+    return hipGetLastError();
+  }
   const int64_t blocks = split_units(split);
-  seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(a, s, n_qt, split);
+  seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(b, s, n_qt, split);
   return hipGetLastError();
 }
 

@@ -73,6 +73,51 @@ def _fused_qk_dot_mode_id() -> int:
     raise ValueError("REAL_PRUNING_FUSED_QK_DOT_MODE must be one of: bf16, tf32, fp32")
 
 
+PLAN_INTS = 8
+
+
+def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, batch_size: int,
+                             current_len: int, capacity: int, device=None, slots: Optional[int] = None):
+    """Work plan of :func:`fused_real_pruning_flat_segmented_attention` for
+    host copies of its offset tables (``[H, S]``, ``[H]``; torch CPU tensors
+    or numpy arrays), ``batch_size``, ``current_len`` and slab ``capacity``:
+    an int32 tensor ``[units, 8]`` on ``device`` (host when None) to pass as
+    ``work_plan`` with every call on those tables.  Built on the host by
+    ``hkv_segmented_attention_plan``; ``slots`` defaults to the device's
+    resident attention workgroups.  No counterpart in the reference, whose
+    Triton grid walks the tables directly."""
+    import numpy as np
+
+    def host(t):
+        a = t.detach().cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t)
+        return np.ascontiguousarray(a, dtype=np.int32)
+
+    st, en, ct = host(segment_starts), host(segment_ends), host(segment_counts)
+    if st.ndim != 2 or st.shape != en.shape or ct.shape != (st.shape[0],):
+        raise ValueError("segment tables must be [H, S], [H, S] and [H]")
+    lib = _lib.load()
+    if slots is None:
+        if device is None:
+            raise ValueError("segmented_attention_plan needs a device or slots")
+        dev = torch.device(device)
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        slots = int(lib.hkv_segmented_attention_slots(idx))
+        if slots < 0:
+            _lib.check(slots)
+    H, S = st.shape
+    args = (st.ctypes.data, en.ctypes.data, ct.ctypes.data, H, S, int(capacity), int(batch_size),
+            int(current_len), int(slots))
+    n = int(lib.hkv_segmented_attention_plan(*args, None, 0))
+    if n < 0:
+        _lib.check(n)
+    plan = np.zeros((max(n, 1), PLAN_INTS), dtype=np.int32)
+    n = int(lib.hkv_segmented_attention_plan(*args, plan.ctypes.data, plan.shape[0]))
+    if n < 0:
+        _lib.check(n)
+    out = torch.from_numpy(plan[:n].copy())
+    return out.to(device) if device is not None else out
+
+
 def pack_flat_segments_kv(
     *,
     dst_k: torch.Tensor,
@@ -165,6 +210,7 @@ def fused_real_pruning_flat_segmented_attention(
     softmax_mode: str = "exp",
     return_lse: bool = False,
     out_dtype: Optional[torch.dtype] = None,
+    work_plan: Optional[torch.Tensor] = None,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
 
@@ -172,7 +218,10 @@ def fused_real_pruning_flat_segmented_attention(
     are row offsets into that slab grouped per head, ``segment_counts [H]``.
     Returns ``[B, L, H*D]`` in q's dtype, or ``out_dtype`` (an extension: the
     fp32 result rounded once to bf16 / fp16, what casting q's-dtype output
-    would give), and ``lse [B, H, L]`` fp32 when ``return_lse``.  Mirrors fused_real_pruning_flat_segmented_attention
+    would give), and ``lse [B, H, L]`` fp32 when ``return_lse``.  ``work_plan``
+    (an extension): the plan :func:`segmented_attention_plan` built for these
+    same tables, batch size and current length, on q's device; the kernel then
+    skips ordering its work itself.  Mirrors fused_real_pruning_flat_segmented_attention
     (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
     ``hkv_segmented_attention``.
     """
@@ -262,6 +311,12 @@ def fused_real_pruning_flat_segmented_attention(
         if return_lse
         else None
     )
+    if work_plan is not None:
+        if (work_plan.dtype != torch.int32 or work_plan.ndim != 2 or work_plan.shape[1] != PLAN_INTS
+                or not work_plan.is_contiguous()):
+            raise ValueError(f"work_plan must be a contiguous int32 tensor [units, {PLAN_INTS}]")
+        if work_plan.device != q.device:
+            raise ValueError("work_plan must be on the same device as q")
     stream = torch.cuda.current_stream(q.device)
     ws = _lib.attention_workspace(q.device, stream)
     code = _lib.load().hkv_segmented_attention(
@@ -273,6 +328,8 @@ def fused_real_pruning_flat_segmented_attention(
         int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
         _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
         _lib.dtype_code(out_dtype), float(softmax_scale), 1 if softmax_mode == "exp2" else 0, qk_mode, value_mode,
+        work_plan.data_ptr() if work_plan is not None else None,
+        int(work_plan.shape[0]) if work_plan is not None else 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         stream.cuda_stream,
     )

@@ -36,6 +36,7 @@ from . import phase_profile as prof
 from .real_pruning_fused_attention import (
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
+    segmented_attention_plan,
 )
 from .slab_schedule import CopyPlan, SlabSchedule
 
@@ -52,6 +53,15 @@ def _env_flag(name: str, default: bool) -> bool:
 def baseline_prefix_enabled() -> bool:
     """REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX (default on; enable_real_pruning_fast.py:1062-1066)."""
     return _env_flag("REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX", True)
+
+
+def work_plans_enabled(device) -> bool:
+    """HKV_ATTN_PLAN (default on): attention calls on a GPU carry a host work
+    plan of their (static) tables, built once per tables, batch and length --
+    not while a HIP graph is being captured (a plan not built before the
+    capture is left out: its upload would be a captured host copy)."""
+    return (_env_flag("HKV_ATTN_PLAN", True) and torch.device(device).type == "cuda"
+            and not torch.cuda.is_current_stream_capturing())
 
 
 def fused_softmax_mode() -> str:
@@ -151,41 +161,51 @@ class SegmentedLayerCache:
 
     # ------------------------------------------------------------------ attention
 
-    def _dense_tables(self, heads: int, T: int, device):
-        """Offset tables that present a dense cache ``[B, H, T, D]`` as a slab ``[B, H*T, D]``."""
-        key = (heads, T, str(device))
+    def _dense_tables(self, heads: int, T: int, device, batch: int, L: int):
+        """Offset tables that present a dense cache ``[B, H, T, D]`` as a slab
+        ``[B, H*T, D]``, and their work plan for ``batch`` x ``L`` queries."""
+        key = (heads, T, str(device), batch, L)
         hit = self._tables_by_len.get(key)
         if hit is None:
             starts = (torch.arange(heads, dtype=torch.int32) * T).reshape(heads, 1)
-            hit = (starts.to(device), (starts + T).to(device),
-                   torch.ones((heads,), dtype=torch.int32).to(device))
+            ends = starts + T
+            counts = torch.ones((heads,), dtype=torch.int32)
+            plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
+                                             capacity=heads * T, device=device)
+                    if work_plans_enabled(device) else None)
+            hit = (starts.to(device), ends.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
 
-    def _empty_tables(self, heads: int, device):
-        """Tables with no segment (attention over the current scale only), made once."""
-        key = ("empty", heads, str(device))
+    def _empty_tables(self, heads: int, device, batch: int, L: int):
+        """Tables with no segment (attention over the current scale only) and
+        their work plan, made once."""
+        key = ("empty", heads, str(device), batch, L)
         hit = self._tables_by_len.get(key)
         if hit is None:
-            empty = torch.zeros((heads, 0), dtype=torch.int32, device=device)
-            hit = (empty, empty, torch.zeros((heads,), dtype=torch.int32, device=device))
+            empty = torch.zeros((heads, 0), dtype=torch.int32)
+            counts = torch.zeros((heads,), dtype=torch.int32)
+            plan = (segmented_attention_plan(empty, empty, counts, batch_size=batch, current_len=L, capacity=0,
+                                             device=device)
+                    if work_plans_enabled(device) else None)
+            hit = (empty.to(device), empty.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
 
     def _attend_dense(self, q, k, v, scale, mode, out_dtype=None):
         B, H, L, D = q.shape
         if self.cached_k is None or self.logical_len == 0:
-            tables = self._empty_tables(H, q.device)
+            tables = self._empty_tables(H, q.device, B, L)
             slab_k = slab_v = None
         else:
             T = self.cached_k.shape[2]
-            tables = self._dense_tables(H, T, q.device)
+            tables = self._dense_tables(H, T, q.device, B, L)
             slab_k = self.cached_k.reshape(B, H * T, D)
             slab_v = self.cached_v.reshape(B, H * T, D)
         return fused_real_pruning_flat_segmented_attention(
             q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=tables[0],
             segment_ends=tables[1], segment_counts=tables[2], current_k=k, current_v=v,
-            softmax_scale=scale, softmax_mode=mode, out_dtype=out_dtype)
+            softmax_scale=scale, softmax_mode=mode, out_dtype=out_dtype, work_plan=tables[3])
 
     # ------------------------------------------------------------------ step
 
@@ -256,12 +276,14 @@ class SegmentedLayerCache:
                 if not self.active:
                     self._activate_from_dense(self.cached_k, self.cached_v, scale_ind)
                 starts, ends, counts = self.schedule.device_tables(scale_ind, q.device)
+                plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]))
+                        if work_plans_enabled(q.device) else None)
             with prof.phase("attention"):
                 out = fused_real_pruning_flat_segmented_attention(
                     q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
                     segment_starts=starts, segment_ends=ends, segment_counts=counts,
                     current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
-                    out_dtype=out_dtype)
+                    out_dtype=out_dtype, work_plan=plan)
 
         with prof.phase("compact"):
             if final:

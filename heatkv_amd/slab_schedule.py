@@ -133,6 +133,21 @@ class SlabSchedule:
             self._device_cache[key] = hit
         return hit
 
+    def device_work_plan(self, target: int, device, batch: int, cur_len: int) -> torch.Tensor:
+        """Attention work plan of ``target``'s tables for ``batch`` rows of
+        ``cur_len`` queries on ``device`` (segmented_attention_plan), built on
+        the host and moved once, cached."""
+        from .real_pruning_fused_attention import segmented_attention_plan
+
+        key = ("work_plan", str(device), int(target), int(batch), int(cur_len))
+        hit = self._device_cache.get(key)
+        if hit is None:
+            st, en, ct = self.tables[int(target)]
+            hit = segmented_attention_plan(st, en, ct, batch_size=batch, current_len=cur_len,
+                                           capacity=self.capacity, device=device)
+            self._device_cache[key] = hit
+        return hit
+
     def fused_append(self, scale: int, device) -> Tuple[Optional[torch.Tensor], CopyPlan]:
         """Split of the append of ``scale`` (plan ``(scale, scale + 1)``) for a
         producer that writes K/V rows before this scale's attention runs.

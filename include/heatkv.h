@@ -99,6 +99,13 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *              V's type (fp32 V: P and V in 2 bf16 pieces, beyond the
  *              reference's TF32 dot), 2 = an fp32 P V product (P in 3 pieces,
  *              V in as many as its type needs).
+ *   work_plan, plan_units : NULL / 0 (the kernel orders its work from the
+ *              tables itself), or a device copy of the plan that
+ *              hkv_segmented_attention_plan built from host copies of these
+ *              same tables, batch and cur_len: one workgroup per unit, no
+ *              planning in the kernel.  Only the 16-bit kernel uses it (fp32 K
+ *              or V, and the fp32 value mode, plan in the kernel).  A plan for
+ *              other tables gives wrong results but stays inside the tensors.
  *   workspace, workspace_bytes : NULL / 0, or device memory of at least
  *              hkv_segmented_attention_workspace_bytes(device) bytes whose
  *              first 64 KiB (per-item counters) are zero before its first
@@ -124,7 +131,32 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
                                 int32_t out_dtype, float softmax_scale, int32_t use_exp2,
                                 int32_t qk_dot_mode, int32_t value_dot_mode,
+                                const int32_t* work_plan, int32_t plan_units,
                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+/*
+ * Work plan of hkv_segmented_attention for host copies of its offset tables
+ * (int32 seg_starts / seg_ends [heads, max_segments], seg_counts [heads]),
+ * batch and cur_len, for a device with `slots` resident attention workgroups
+ * (hkv_segmented_attention_slots; 0 = cut nothing): writes plan units of 8
+ * int32 each into `units` (host memory, room for max_units) and returns
+ * their count, or only the count when `units` is NULL; a negative HKV_ERR_*
+ * code on bad arguments.  Items (batch row, head, 128-query tile) are ordered
+ * heaviest head first; when a launch has under four rounds of items per
+ * slot, the heaviest items may be cut into two key-range parts chosen by
+ * simulating the dispatch.  Host-only: no device call.  No counterpart in
+ * the reference (its tables are the whole plan: the Triton grid walks them).
+ */
+int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
+                                     const int32_t* seg_counts, int32_t heads, int32_t max_segments,
+                                     int64_t slab_capacity, int32_t batch, int32_t cur_len, int32_t slots,
+                                     int32_t* units, int32_t max_units);
+
+/* Resident attention workgroups of `device` (2 per CU), the `slots` of
+ * hkv_segmented_attention_plan; a negative HKV_ERR_* code when the device
+ * cannot be queried.  No counterpart in the reference. */
+int32_t hkv_segmented_attention_slots(int32_t device);
 
 /*
  * Bytes of the hkv_segmented_attention workspace for `device` (64 KiB of
@@ -156,7 +188,7 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
                                         int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
                                         int32_t v_dtype, int32_t out_dtype, float softmax_scale,
                                         int32_t use_exp2, int32_t qk_dot_mode, int32_t value_dot_mode,
-                                        void* stream);
+                                        const int32_t* work_plan, int32_t plan_units, void* stream);
 
 /*
  * QKV producer epilogue of one scale: from the QKV projection output to the

@@ -56,23 +56,23 @@ def test_argument_errors_before_any_device_call():
     null = None
     # head_dim 64 -> unsupported (RuntimeError in Python)
     code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
-                                       1, 1, 1, 0, 0, 64, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null)
+                                       1, 1, 1, 0, 0, 64, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null, 0, null)
     assert code == _lib.HKV_ERR_UNSUPPORTED and "head_dim=128" in _lib.last_error()
     with pytest.raises(RuntimeError, match="head_dim=128"):
         _lib.check(code)
     # q/k dtype mismatch
     code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
-                                       1, 1, 1, 0, 0, 128, 3, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null)
+                                       1, 1, 1, 0, 0, 128, 3, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null, 0, null)
     assert code == _lib.HKV_ERR_UNSUPPORTED
     # null pointers -> invalid argument (ValueError)
     code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
-                                       1, 1, 1, 0, 0, 128, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null)
+                                       1, 1, 1, 0, 0, 128, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null, 0, null)
     assert code == _lib.HKV_ERR_INVALID_ARG
     with pytest.raises(ValueError):
         _lib.check(code)
     # too many segments
     code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
-                                       1, 1, 1, 10, 300, 128, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null)
+                                       1, 1, 1, 10, 300, 128, 2, 2, 2, 0, ctypes.c_float(1.0), 0, 0, 0, null, 0, null, 0, null)
     assert code == _lib.HKV_ERR_UNSUPPORTED and "max_segments" in _lib.last_error()
     # pack: empty work is a no-op success, bad head_dim / element size rejected
     assert lib.hkv_pack_segments(null, null, null, null, 0, 0, 0, 0, 1, 128, 2, 2, null, null, null,
@@ -85,13 +85,13 @@ def test_argument_errors_before_any_device_call():
                                  3, 10, null) == _lib.HKV_ERR_INVALID_ARG
     # bad output dtype
     code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
-                                       1, 1, 1, 0, 0, 128, 2, 2, 2, 7, ctypes.c_float(1.0), 0, 0, 0, null, 0, null)
+                                       1, 1, 1, 0, 0, 128, 2, 2, 2, 7, ctypes.c_float(1.0), 0, 0, 0, null, 0, null, 0, null)
     assert code == _lib.HKV_ERR_UNSUPPORTED and "out_dtype" in _lib.last_error()
     # dot modes outside the reference's ids
     for qk, vm in ((3, 0), (-1, 0), (0, 1), (0, 3)):
         code = lib.hkv_segmented_attention(null, null, null, null, null, null, null, null, null, null,
                                            1, 1, 1, 0, 0, 128, 2, 2, 2, 0, ctypes.c_float(1.0), 0, qk, vm,
-                                           null, 0, null)
+                                           null, 0, null, 0, null)
         assert code == _lib.HKV_ERR_INVALID_ARG and "dot_mode" in _lib.last_error()
     # without a device the workspace size cannot be queried
     if not torch.cuda.is_available():

@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 import torch
 
-from heatkv_amd import _lib
+from heatkv_amd import _lib, segmented_attention_plan
 from heatkv_amd import workloads as W
 from oracle import segmented_attention as oattn
 from support import assert_attention_close, to_np
@@ -31,8 +31,9 @@ pytestmark = pytest.mark.gpu
 ORACLE_WORKERS = 16
 
 
-def abi_attention(wl, device, *, workspace=True):
-    """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse."""
+def abi_attention(wl, device, *, workspace=True, planned=False):
+    """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse
+    (``planned``: with the host work plan of its tables)."""
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
@@ -40,12 +41,18 @@ def abi_attention(wl, device, *, workspace=True):
     out = torch.full((B, L, H * D), float("nan"), dtype=q.dtype, device=device)
     lse = torch.full((B, H, L), float("nan"), dtype=torch.float32, device=device)
     ws = _lib.attention_workspace(device) if workspace else None
+    plan = None
+    if planned:
+        hst, hen, hct = wl.tables()
+        plan = segmented_attention_plan(hst, hen, hct, batch_size=B, current_len=L,
+                                        capacity=wl.schedule.capacity, device=device)
     stream = torch.cuda.current_stream(device)
     code = _lib.load().hkv_segmented_attention(
         q.data_ptr(), slab_k.data_ptr(), slab_v.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
         ck.data_ptr(), cv.data_ptr(), out.data_ptr(), lse.data_ptr(), B, H, L, int(slab_k.shape[1]),
         int(st.shape[1]), D, _lib.dtype_code(q.dtype), _lib.dtype_code(ck.dtype), _lib.dtype_code(cv.dtype), 0,
-        float(wl.softmax_scale), 0, 0, 0, ws.data_ptr() if ws is not None else None,
+        float(wl.softmax_scale), 0, 0, 0, plan.data_ptr() if plan is not None else None,
+        int(plan.shape[0]) if plan is not None else 0, ws.data_ptr() if ws is not None else None,
         int(ws.numel()) if ws is not None else 0, stream.cuda_stream)
     _lib.check(code)
     torch.cuda.synchronize(device)
@@ -98,3 +105,18 @@ def test_every_row_8b_class(budget, device):
 
 def test_every_row_skewed_ragged(device):
     check_every_row(W.config(5), device)
+
+
+# With the host work plan (its cut items and XCD grouping) instead of the
+# kernel's own ordering.
+def test_every_row_2b_final_planned(device):
+    check_every_row(W.config(2), device, planned=True)
+
+
+@pytest.mark.parametrize("budget", [0.1, 1.0])
+def test_every_row_8b_class_planned(budget, device):
+    check_every_row(_config4(budget), device, planned=True)
+
+
+def test_every_row_skewed_ragged_planned(device):
+    check_every_row(W.config(5), device, planned=True)

@@ -365,7 +365,7 @@ def test_attention_output_not_16_byte_aligned(split, device, monkeypatch):
     code = _lib.load().hkv_segmented_attention(
         qd.data_ptr(), skd.data_ptr(), svd.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
         ckd.data_ptr(), cvd.data_ptr(), buf.data_ptr() + 8, None, B, H, L, cap, S, 128,
-        _lib.dtype_code(qd.dtype), _lib.dtype_code(ckd.dtype), _lib.dtype_code(cvd.dtype), 0, float(scale), 0, 0, 0,
+        _lib.dtype_code(qd.dtype), _lib.dtype_code(ckd.dtype), _lib.dtype_code(cvd.dtype), 0, float(scale), 0, 0, 0, None, 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
         stream.cuda_stream)
     _lib.check(code)
@@ -396,3 +396,30 @@ def test_attention_random_shapes(seed, device, monkeypatch):
     ref_out, ref_lse = oattn.flat_segmented_attention(
         to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale)
     assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"seed {seed}")
+
+
+@pytest.mark.parametrize("seed", list(range(60, 70)))
+def test_attention_random_shapes_planned(seed, device, monkeypatch):
+    """Random shapes (as above, up to 2300 queries so that items get cut)
+    with the host work plan of their tables, with and without the workspace
+    (without it, cut units run whole), against the oracle."""
+    from heatkv_amd import segmented_attention_plan
+
+    g = torch.Generator().manual_seed(seed)
+
+    def pick(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    B, H, L, cap, S = pick(1, 3), pick(1, 40), pick(1, 2300), pick(0, 5000), pick(0, 40)
+    if cap == 0:
+        S = 0
+    split = "1" if seed % 2 else "0"
+    monkeypatch.setenv("HKV_ATTN_SPLIT", split)
+    print(f"[attn] planned random shape seed={seed} B={B} H={H} L={L} cap={cap} S={S} split={split}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(seed, B, H, L, cap, S)
+    plan = segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device)
+    scale = 1.0 / math.sqrt(128)
+    out, lse = _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan)
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale, workers=16)
+    assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"planned seed {seed}")

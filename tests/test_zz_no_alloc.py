@@ -48,7 +48,7 @@ def _call(entry, case, device, workspace):
     lse = torch.full((B, H, L), float("nan"), dtype=torch.float32, device=device)
     args = [q.data_ptr(), sk.data_ptr(), sv.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
             ck.data_ptr(), cv.data_ptr(), out.data_ptr(), lse.data_ptr(), B, H, L, int(sk.shape[1]),
-            int(st.shape[1]), D, 2, 2, 2, 0, 1.0 / math.sqrt(128), 0, 0, 0]
+            int(st.shape[1]), D, 2, 2, 2, 0, 1.0 / math.sqrt(128), 0, 0, 0, None, 0]
     if workspace is not None:
         args += [workspace.data_ptr(), int(workspace.numel())]
     code = entry(*args, torch.cuda.current_stream(device).cuda_stream)
