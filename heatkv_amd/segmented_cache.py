@@ -57,11 +57,16 @@ def baseline_prefix_enabled() -> bool:
 
 def work_plans_enabled(device) -> bool:
     """HKV_ATTN_PLAN (default on): attention calls on a GPU carry a host work
-    plan of their (static) tables, built once per tables, batch and length --
-    not while a HIP graph is being captured (a plan not built before the
-    capture is left out: its upload would be a captured host copy)."""
-    return (_env_flag("HKV_ATTN_PLAN", True) and torch.device(device).type == "cuda"
-            and not torch.cuda.is_current_stream_capturing())
+    plan of their (static) tables, built once per tables, batch and length.
+    While a HIP graph is being captured no plan is built (its upload would be
+    a captured host copy): a call uses the plan made by an eager call before
+    the capture, so that replays compute exactly what eager calls compute,
+    and none if there was no such call."""
+    return _env_flag("HKV_ATTN_PLAN", True) and torch.device(device).type == "cuda"
+
+
+def _capturing() -> bool:
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
 def fused_softmax_mode() -> str:
@@ -172,7 +177,7 @@ class SegmentedLayerCache:
             counts = torch.ones((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
                                              capacity=heads * T, device=device)
-                    if work_plans_enabled(device) else None)
+                    if work_plans_enabled(device) and not _capturing() else None)
             hit = (starts.to(device), ends.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
@@ -187,7 +192,7 @@ class SegmentedLayerCache:
             counts = torch.zeros((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(empty, empty, counts, batch_size=batch, current_len=L, capacity=0,
                                              device=device)
-                    if work_plans_enabled(device) else None)
+                    if work_plans_enabled(device) and not _capturing() else None)
             hit = (empty.to(device), empty.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
@@ -276,7 +281,8 @@ class SegmentedLayerCache:
                 if not self.active:
                     self._activate_from_dense(self.cached_k, self.cached_v, scale_ind)
                 starts, ends, counts = self.schedule.device_tables(scale_ind, q.device)
-                plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]))
+                plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]),
+                                                       build=not _capturing())
                         if work_plans_enabled(q.device) else None)
             with prof.phase("attention"):
                 out = fused_real_pruning_flat_segmented_attention(

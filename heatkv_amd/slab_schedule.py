@@ -133,15 +133,17 @@ class SlabSchedule:
             self._device_cache[key] = hit
         return hit
 
-    def device_work_plan(self, target: int, device, batch: int, cur_len: int) -> torch.Tensor:
+    def device_work_plan(self, target: int, device, batch: int, cur_len: int, *,
+                         build: bool = True) -> Optional[torch.Tensor]:
         """Attention work plan of ``target``'s tables for ``batch`` rows of
         ``cur_len`` queries on ``device`` (segmented_attention_plan), built on
-        the host and moved once, cached."""
+        the host and moved once, cached.  With ``build=False`` only a plan
+        already made is returned (None otherwise)."""
         from .real_pruning_fused_attention import segmented_attention_plan
 
         key = ("work_plan", str(device), int(target), int(batch), int(cur_len))
         hit = self._device_cache.get(key)
-        if hit is None:
+        if hit is None and build:
             st, en, ct = self.tables[int(target)]
             hit = segmented_attention_plan(st, en, ct, batch_size=batch, current_len=cur_len,
                                            capacity=self.capacity, device=device)

@@ -2,9 +2,10 @@
 
 Checks, for the benchmark workloads and random tables: every (batch row,
 head, 128-query tile) item's key tiles are covered exactly once by the plan's
-units, a cut item has exactly two parts [0, a) and [a, n) with one counter
-index each, counters are dense and below the slot count, whole items come
-first heaviest head first, and the tile counts are those of the tables
+units (empty units, head -1, leave at once), a cut item has exactly two parts
+[0, a) and [a, n) with one counter index each, counters are dense and below
+the slot count, on each XCD (unit id % 8) whole items come first heaviest
+first and parts longest first, and the tile counts are those of the tables
 (ceil(R_h / 64) + ceil(L / 64), with R_h the clamped retained rows).
 """
 
@@ -42,6 +43,9 @@ def _check(plan, st, en, ct, B, L, cap, slots):
     cover = {}
     cuts = {}
     for h, j, t0, t1, cut, part, z0, z1 in plan.tolist():
+        if h == -1:  # an empty unit
+            assert (j, t0, t1, cut, part, z0, z1) == (-1, 0, 0, -1, 0, 0, 0)
+            continue
         assert 0 <= h < H and 0 <= j < B * n_qt and z0 == 0 and z1 == 0
         assert 0 <= t0 < t1 <= tiles[h]
         cover.setdefault((h, j), []).append((t0, t1))
@@ -60,16 +64,21 @@ def _check(plan, st, en, ct, B, L, cap, slots):
         assert len(ps) == 2 and ps[0][:2] == ps[1][:2] and {p[2] for p in ps} == {0, 1}
         first = [p for p in ps if p[2] == 0][0]
         assert first[3] == 0 and first[4] - first[3] >= 8 and tiles[first[0]] - first[4] >= 8
-    # whole units come first, heaviest head first (before the XCD grouping of
-    # plans without cuts, which permutes within groups of equal work)
-    whole = [u for u in plan.tolist() if u[4] < 0]
-    cutu = [u for u in plan.tolist() if u[4] >= 0]
-    assert plan.tolist()[:len(whole)] == whole
-    if cutu:
-        sizes = [tiles[u[0]] for u in whole]
-        assert sizes == sorted(sizes, reverse=True)
-        lens = [u[3] - u[2] for u in cutu]
-        assert lens == sorted(lens, reverse=True)
+    # on each XCD whole units come first, heaviest head first, then the parts
+    # longest first (plans without cuts are permuted into XCD groups of equal
+    # work instead)
+    if cuts:
+        units = plan.tolist()
+        for x in range(8):
+            mine = [u for u in units[x::8] if u[0] >= 0]
+            whole = [u for u in mine if u[4] < 0]
+            assert mine[:len(whole)] == whole
+            sizes = [tiles[u[0]] for u in whole]
+            assert sizes == sorted(sizes, reverse=True)
+            lens = [u[3] - u[2] for u in mine[len(whole):]]
+            assert lens == sorted(lens, reverse=True)
+    # empty units only pad the XCD lists: fewer than 8 per unit index
+    assert (plan[:, 0] < 0).sum() < 8 * max(1, -(-len(plan) // 8))
     return len(cuts)
 
 
@@ -89,12 +98,21 @@ def test_plan_of_benchmark_workloads(cfg):
 def test_plan_cuts_the_2b_final_step():
     """The 2B final step (1024 items, two rounds of 512 slots, two heads with
     1.8x the others' key tiles) is cut; without cuts list scheduling ends at
-    184 tile times against an average of 145."""
+    184 tile times against an average of 145.  Its items are dealt to XCDs in
+    chunks of at least a quarter of a group: each (batch row, head) group's
+    units land on at most 4 of the 8 XCDs, and every XCD list is padded to
+    the same length."""
     wl = W.config(2)
     st, en, ct = (t.numpy() for t in wl.tables())
     plan = segmented_attention_plan(st, en, ct, batch_size=2, current_len=4096, capacity=wl.schedule.capacity,
                                     slots=512)
     assert _check(plan, st, en, ct, 2, 4096, wl.schedule.capacity, 512) > 0
+    assert len(plan) % 8 == 0
+    xcds = {}
+    for i, (h, j) in enumerate(plan[:, :2].tolist()):
+        if h >= 0:
+            xcds.setdefault((h, j // 32), set()).add(i % 8)
+    assert len(xcds) == 32 and max(len(v) for v in xcds.values()) <= 4
 
 
 @pytest.mark.parametrize("seed", range(8))
