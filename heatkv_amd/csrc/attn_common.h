@@ -201,6 +201,9 @@ __device__ __forceinline__ void length_prefix(int32_t* seg_pref, int nseg, int l
 
 // Head h's clamped segment starts and exclusive length prefix into LDS (ends
 // with a workgroup barrier); returns the live entry count, w.R = its total.
+// The count and the head's S table entries are loaded together (entries past
+// the count are read and dropped), so the launch waits for one round trip,
+// not two.
 template <int kThreads>
 __device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ seg_starts,
                                                    const int32_t* __restrict__ seg_ends,
@@ -211,15 +214,17 @@ __device__ __forceinline__ void load_head_segments(const int32_t* __restrict__ s
   const int lane = tid & 63;
   const int wave = tid >> 6;
   int nseg = seg_counts[w.h];
-  nseg = nseg < 0 ? 0 : (nseg > S ? S : nseg);
-  for (int i = tid; i < nseg; i += kThreads) {
+  for (int i = tid; i < S; i += kThreads) {
     int64_t st = seg_starts[static_cast<int64_t>(w.h) * S + i];
     int64_t en = seg_ends[static_cast<int64_t>(w.h) * S + i];
     st = st < 0 ? 0 : (st > cap ? cap : st);
     en = en < 0 ? 0 : (en > cap ? cap : en);
-    seg_start[i] = static_cast<int32_t>(st);
-    seg_pref[i + 1] = en > st ? static_cast<int32_t>(en - st) : 0;
+    if (i < nseg) {
+      seg_start[i] = static_cast<int32_t>(st);
+      seg_pref[i + 1] = en > st ? static_cast<int32_t>(en - st) : 0;
+    }
   }
+  nseg = nseg < 0 ? 0 : (nseg > S ? S : nseg);
   __syncthreads();
   if (wave == 0) length_prefix(seg_pref, nseg, lane);
   __syncthreads();

@@ -222,34 +222,31 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   WorkItem w;
   int32_t t_begin, t_end, parts;
   const int32_t ntc = (L + kBN - 1) / kBN;
-  if (a.plan != nullptr) {
+  // An item's key stream: its ntc current-scale tiles first (addressed
+  // without any table), then its R retained prior rows, ntp tiles through the
+  // row tables.
+  const bool planned = a.plan != nullptr;
+  int32_t p0 = 0, p1 = 0;
+  bool cut = false;
+  if (planned) {
     // the unit of this workgroup from the caller's work plan
     const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
-    const int32_t ph = pu[0], pj = pu[1], p0 = pu[2], p1 = pu[3], pcut = pu[4], ppart = pu[5];
+    const int32_t ph = pu[0], pj = pu[1], pcut = pu[4], ppart = pu[5];
+    p0 = pu[2];
+    p1 = pu[3];
     if (ph < 0 || ph >= H || pj < 0 || pj >= a.batch * n_qt) return;  // not a unit of this launch
     w.h = ph;
     w.b = pj / n_qt;
     w.qt = pj - w.b * n_qt;
     w.bh = w.b * H + w.h;
-    load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
-                                 seg_pref);
-    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
-    t_begin = p0 < 0 ? 0 : (p0 > ntiles ? ntiles : p0);
-    t_end = p1 < t_begin ? t_begin : (p1 > ntiles ? ntiles : p1);
     // a cut item's record and counter exist when the launch has a workspace
-    const bool cut = pcut >= 0 && a.workspace != nullptr && pcut < a.ws_cuts && ppart >= 0 &&
-                     ppart < 2;
+    cut = pcut >= 0 && a.workspace != nullptr && pcut < a.ws_cuts && ppart >= 0 && ppart < 2;
     parts = cut ? 2 : 1;
     un.item = 0;
     un.part = cut ? ppart : 0;
     un.parts = parts;
     un.record = cut ? 2 * pcut : 0;
     un.counter = cut ? pcut : 0;
-    if (!cut) {  // a whole item, whatever the plan's range says
-      t_begin = 0;
-      t_end = ntiles;
-    }
-    if (t_begin >= t_end && !cut) return;
   } else {
     un = split_unit(split, static_cast<int32_t>(blockIdx.x));
     if (split.two == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);
@@ -257,27 +254,6 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H, a.max_segments, a.batch, n_qt,
                             head_rows, head_rows + kMaxHeads, seg_start, seg_pref, un.item,
                             head_rows + 2 * kMaxHeads, NS * kStageBytes / 4 - 2 * kMaxHeads);
-    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
-    // A part needs kMinPartTiles key tiles to pay for its record and the
-    // merge, so a short item runs as fewer parts (one, below two such runs);
-    // every part of the item sees the same tile count and agrees.  Parts past
-    // the count leave at once.
-    parts = ntiles / kMinPartTiles;
-    parts = parts < 1 ? 1 : (parts < un.parts ? parts : un.parts);
-    if (un.part >= parts) return;
-    t_begin = un.part * ntiles / parts;
-    t_end = (un.part + 1) * ntiles / parts;
-  }
-  const int32_t R = w.R;
-  const int32_t ntp = (R + kBN - 1) / kBN;
-  if (t_begin >= t_end) {
-    // a planned part with no key tiles (a plan that does not match these
-    // tables): its record is empty -- zero weight in the merge
-    const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
-    f32x16_t none[4] = {};
-    merge_parts<QDT, kThreads>(a, sc, un, parts, none, -1e30f, 0.f, w, qrow, L, H, g, merge_turn,
-                               ring + wave * 32 * kOutPitch);
-    return;
   }
 
   const bool k_wave = wave * kDmaPerWave < 16;
@@ -310,23 +286,23 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   }
   const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
 
-  // This wave's tensor (K or V) of tile `tile` into stage tile % 2.
-  auto issue_tile = [&](int tile) {
-    const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
-    if (tile < ntp) {
-      const int32_t* rt = rowtab[tile % 3];
+  // This wave's tensor (K or V) of current-scale tile c into stage c % 2.
+  auto issue_cur = [&](int c) {
+    const uint32_t dst = ring_lds + (c % NS) * kStageBytes;
+    const uint32_t skip = static_cast<uint32_t>(c) * (kBN * kD * 2);
+    const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
-    } else {
-      const uint32_t skip = static_cast<uint32_t>(tile - ntp) * (kBN * kD * 2);
-      const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
-    }
+    for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
   };
-  auto valid_of = [&](int t) { return t < ntp ? min(kBN, R - t * kBN) : min(kBN, L - (t - ntp) * kBN); };
+  // A planned unit whose first tile is a current-scale one (every whole item,
+  // and a part that starts there) issues it before the head's segment tables
+  // are loaded, and Q with it: the tables, the tile and Q arrive in one round
+  // trip.
+  const int32_t first = cut ? (p0 < 0 ? 0 : p0) : 0;
+  const bool early = planned && first < ntc;
+  if (early) issue_cur(first);
 
-  // Q first: its loads are in flight while wave 0 fills the row tables
+  // Q: its loads are in flight while the tables load and wave 0 fills the row tables
   const int32_t qrow = w.qt * kBM + wave * 32 + (lane & 31);
   u32x4_t qf[8];
   {
@@ -335,13 +311,66 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = load8<QDT, MQK>(rq, qrow < L ? (qrow * kD + ks * 16 + g * 8) * 2 : -1);
   }
+
+  if (planned) {
+    load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
+                                 seg_pref);
+    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
+    t_begin = p0 < 0 ? 0 : (p0 > ntiles ? ntiles : p0);
+    t_end = p1 < t_begin ? t_begin : (p1 > ntiles ? ntiles : p1);
+    if (!cut) {  // a whole item, whatever the plan's range says
+      t_begin = 0;
+      t_end = ntiles;
+    }
+    if (t_begin >= t_end && !cut) {
+      wait_vmcnt<0>();  // the early tile lands before the workgroup's LDS is released
+      return;
+    }
+  } else {
+    const int32_t ntiles = (w.R + kBN - 1) / kBN + ntc;
+    // A part needs kMinPartTiles key tiles to pay for its record and the
+    // merge, so a short item runs as fewer parts (one, below two such runs);
+    // every part of the item sees the same tile count and agrees.  Parts past
+    // the count leave at once.
+    parts = ntiles / kMinPartTiles;
+    parts = parts < 1 ? 1 : (parts < un.parts ? parts : un.parts);
+    if (un.part >= parts) return;
+    t_begin = un.part * ntiles / parts;
+    t_end = (un.part + 1) * ntiles / parts;
+  }
+  const int32_t R = w.R;
+  if (t_begin >= t_end) {
+    // a planned part with no key tiles (a plan that does not match these
+    // tables): its record is empty -- zero weight in the merge
+    wait_vmcnt<0>();
+    f32x16_t none[4] = {};
+    merge_parts<QDT, kThreads>(a, sc, un, parts, none, -1e30f, 0.f, w, qrow, L, H, g, merge_turn,
+                               ring + wave * 32 * kOutPitch);
+    return;
+  }
+
+  // This wave's tensor (K or V) of tile `tile` into stage tile % 2.
+  auto issue_tile = [&](int tile) {
+    if (tile < ntc) {
+      issue_cur(tile);
+      return;
+    }
+    const int p = tile - ntc;
+    const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
+    const int32_t* rt = rowtab[p % 3];
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
+  };
+  auto valid_of = [&](int t) { return t < ntc ? min(kBN, L - t * kBN) : min(kBN, R - (t - ntc) * kBN); };
+
   int cur_seg = 0;
   if (wave == 0) {
-    for (int p = t_begin; p < t_begin + 3 && p < ntp && p < t_end; ++p)
-      fill_rowtab<kD * 2>(p, rowtab[p % 3], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
+    for (int t = t_begin; t < t_begin + 3 && t < t_end; ++t)
+      if (t >= ntc)
+        fill_rowtab<kD * 2>(t - ntc, rowtab[(t - ntc) % 3], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
   }
   __syncthreads();
-  issue_tile(t_begin);
+  if (!early) issue_tile(t_begin);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) qf[ks] ^= sc.q_sign;
 
@@ -401,8 +430,9 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     } else {
       if (t + 1 < t_end) issue_tile(t + 1);
     }
-    if (wave == 0 && t + 3 < ntp && t + 3 < t_end)
-      fill_rowtab<kD * 2>(t + 3, rowtab[(t + 3) % 3], cur_seg, w.nseg, R, seg_start, seg_pref, kPastEnd);
+    if (wave == 0 && t + 3 < t_end && t + 3 >= ntc)
+      fill_rowtab<kD * 2>(t + 3 - ntc, rowtab[(t + 3 - ntc) % 3], cur_seg, w.nseg, R, seg_start, seg_pref,
+                          kPastEnd);
     u32x4_t pf[4];
     qk(snext, t + 1);
     exp_tile(scur, m_run, sc.c, l_run);
