@@ -746,6 +746,119 @@ struct Scalars {
 // average, while -inf still masks the keys past a tile's end.
 constexpr float kMinC = 1e-30f;
 
+// s_waitcnt for "at most n vector-memory operations outstanding" (gfx9
+// encoding; expcnt and lgkmcnt left at their maxima = not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Agent-scope relaxed loads and stores of the partial records and counters:
+// coherent across the XCDs' L2 caches without writing back or invalidating
+// them.
+//
+// Ordering of a record before its counter.  Every word of a record is written
+// by an agent-scope atomic store (global_store ... sc1: written through to the
+// device's coherence point) and read by an agent-scope atomic load (sc1: read
+// from it).  The publishing workgroup waits for its stores to be acknowledged
+// (s_waitcnt vmcnt(0), which on gfx9 counts stores) and for every wave
+// (barrier) before its counter add is issued; the merging workgroup issues its
+// record loads only after it has seen the counter's returned value (barrier).
+// So the hardware orders the record before the counter.  The memory model's
+// way of saying it, an acq_rel counter add, adds a write-back and an
+// invalidate of the whole XCD L2 (buffer_wbl2 / buffer_inv sc1) per part,
+// which protects no data here (nothing in a record is written by a plain
+// store) and costs 2.5% of the 2B final step (310 -> 317 us, 768 parts).
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Part of a cut item: publish the partial record, count it in, and if it is
+// the item's last part to finish, merge every part and write the output.
+// A record holds 66 * kThreads floats (each thread's 64 accumulators, its
+// running max and its sum); item r's parts use records 2r and 2r + 1.  The
+// output goes through `stage` (32 * kOutPitch bytes per wave) when
+// kStageOut, else straight from registers.
+template <int QDT, int kThreads, bool kStageOut = true>
+__device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc, const Unit& un,
+                                            int32_t parts, const f32x16_t (&oacc)[4], float m_run,
+                                            float l_run, const WorkItem& w, int32_t qrow, int L, int H,
+                                            int g, int32_t& merge_turn, uint8_t* stage) {
+  const int tid = threadIdx.x;
+  int32_t* const counters = static_cast<int32_t*>(a.workspace);
+  float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
+  float* const rec0 = records + static_cast<int64_t>(un.record) * (66 * kThreads);
+  {
+    float* const mine = rec0 + static_cast<int64_t>(un.part) * (66 * kThreads);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) st_agent(mine + (db * 16 + j) * kThreads + tid, oacc[db][j]);
+    st_agent(mine + 64 * kThreads + tid, m_run);
+    st_agent(mine + 65 * kThreads + tid, l_run);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (tid == 0)
+    merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+  __syncthreads();
+  if (!merge_turn) return;
+  // Every part is published: combine the parts in part order (this part's
+  // own values from registers, equal to its record), the same arithmetic
+  // whichever part merges.
+  float mp[4], lp[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const bool other = p < parts && p != un.part;
+    const float* rec = rec0 + static_cast<int64_t>(p) * (66 * kThreads);
+    mp[p] = other ? ld_agent(rec + 64 * kThreads + tid) : m_run;
+    lp[p] = other ? ld_agent(rec + 65 * kThreads + tid) : l_run;
+  }
+  float m_new = mp[0];
+#pragma unroll
+  for (int p = 1; p < 4; ++p)
+    if (p < parts) m_new = fmaxf(m_new, mp[p]);
+  f32x16_t acc[4] = {};
+  float l_acc = 0.f;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if (p >= parts) break;
+    const float al = __builtin_amdgcn_exp2f((mp[p] - m_new) * sc.c);
+    const float* rec = rec0 + static_cast<int64_t>(p) * (66 * kThreads);
+    if (p == un.part) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[db][j] = p == 0 ? oacc[db][j] * al : __builtin_fmaf(oacc[db][j], al, acc[db][j]);
+    } else {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float o = ld_agent(rec + (db * 16 + j) * kThreads + tid);
+          acc[db][j] = p == 0 ? o * al : __builtin_fmaf(o, al, acc[db][j]);
+        }
+    }
+    l_acc = p == 0 ? lp[p] * al : __builtin_fmaf(lp[p], al, l_acc);
+  }
+  if (kStageOut && a.out_dtype != kF32 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+    // the stage is free: every wave passed the barriers above after its last tile
+    const int32_t qrow0 = qrow - (tid & 31);
+    if (a.out_dtype == kF16)
+      write_output_lds<kF16>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, tid & 63, stage);
+    else
+      write_output_lds<kBF16>(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow0, L, H, w.bh, tid & 63, stage);
+  } else {
+    write_output(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+  }
+  if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace attn
 
 hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);

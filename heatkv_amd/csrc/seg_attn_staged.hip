@@ -155,6 +155,7 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   __shared__ int32_t seg_pref[kMaxSegments + 1];
   __shared__ __attribute__((aligned(16))) int32_t head_rows[kMaxHeads];
   __shared__ int32_t head_by_rank[kMaxHeads];
+  __shared__ int32_t merge_turn;
 
   const int64_t cap = a.slab_capacity;
   const int H = a.heads;
@@ -164,14 +165,46 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   const int wave = tid >> 6;
   const int g = lane >> 5;
 
-  const WorkItem w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H,
-                                         a.max_segments, a.batch, n_qt, head_rows, head_by_rank,
-                                         seg_start, seg_pref, static_cast<int32_t>(blockIdx.x),
-                                         reinterpret_cast<int32_t*>(k_lds), sizeof(k_lds) / 4);
+  // The workgroup's unit: from the caller's work plan (a whole item or one
+  // key-range part of a cut item, merged through the workspace as in the
+  // 16-bit kernel), else the workgroup's item in longest-first order.
+  WorkItem w;
+  Unit un{0, 0, 1, 0, 0};
+  int32_t p0 = 0, p1 = 0;
+  if (a.plan != nullptr) {
+    const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
+    const int32_t ph = pu[0], pj = pu[1], pcut = pu[4], ppart = pu[5];
+    p0 = pu[2];
+    p1 = pu[3];
+    if (ph < 0 || ph >= H || pj < 0 || pj >= a.batch * n_qt) return;  // not a unit of this launch
+    w.h = ph;
+    w.b = pj / n_qt;
+    w.qt = pj - w.b * n_qt;
+    w.bh = w.b * H + w.h;
+    const bool cut = pcut >= 0 && a.workspace != nullptr && pcut < a.ws_cuts && ppart >= 0 && ppart < 2;
+    un.part = cut ? ppart : 0;
+    un.parts = cut ? 2 : 1;
+    un.record = cut ? 2 * pcut : 0;
+    un.counter = cut ? pcut : 0;
+    load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
+                                 seg_pref);
+  } else {
+    w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H, a.max_segments, a.batch, n_qt,
+                            head_rows, head_by_rank, seg_start, seg_pref, static_cast<int32_t>(blockIdx.x),
+                            reinterpret_cast<int32_t*>(k_lds), sizeof(k_lds) / 4);
+  }
   const int32_t R = w.R;
   const int32_t ntp = (R + kBN - 1) / kBN;
   const int32_t ntc = (L + kBN - 1) / kBN;
   const int32_t ntiles = ntp + ntc;
+  const int32_t parts = un.parts;
+  int32_t t_begin = 0, t_end = ntiles;
+  if (parts > 1) {
+    t_begin = p0 < 0 ? 0 : (p0 > ntiles ? ntiles : p0);
+    t_end = p1 < t_begin ? t_begin : (p1 > ntiles ? ntiles : p1);
+  }
+  // the output staging of a merge reuses the K buffers once the last tile is done
+  constexpr bool kStageOut = NQS * kKBytes >= NW * 32 * kOutPitch;
 
   const __amdgpu_buffer_rsrc_t rs_k = make_rsrc(
       static_cast<const uint8_t*>(a.slab_k) + static_cast<int64_t>(w.b) * cap * kD * kEK,
@@ -280,16 +313,26 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   const uint8_t* k_lane = k_lds + (lane & 31) * kKPitch + g * 16;
   const uint8_t* v_lane = vt_lds + (lane & 31) * kVtPitch + g * 8;
 
-  if (wave == 0 && ntp > 0) fill_rowtab(0, rowtab[0], cur_seg, w.nseg, R, seg_start, seg_pref);
+  if (t_begin >= t_end) {
+    // a planned part with no key tiles (a plan that does not match these
+    // tables): its record is empty -- zero weight in the merge
+    f32x16_t none[4] = {};
+    merge_parts<QDT, kThreads, kStageOut>(a, sc, un, parts, none, -1e30f, 0.f, w, qrow, L, H, g, merge_turn,
+                                          k_lds + wave * 32 * kOutPitch);
+    return;
+  }
+  if (wave == 0 && t_begin < ntp)
+    fill_rowtab(t_begin, rowtab[t_begin & 1], cur_seg, w.nseg, R, seg_start, seg_pref);
   __syncthreads();
-  issue_loads(0, 0);
-  if (wave == 0 && 1 < ntp) fill_rowtab(1, rowtab[1], cur_seg, w.nseg, R, seg_start, seg_pref);
+  issue_loads(t_begin, t_begin & 1);
+  if (wave == 0 && t_begin + 1 < ntp && t_begin + 1 < t_end)
+    fill_rowtab(t_begin + 1, rowtab[(t_begin + 1) & 1], cur_seg, w.nseg, R, seg_start, seg_pref);
 
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = t_begin; t < t_end; ++t) {
     store_tile();
     __syncthreads();
-    if (t + 1 < ntiles) issue_loads(t + 1, (t + 1) & 1);
-    if (wave == 0 && t + 2 < ntp)
+    if (t + 1 < t_end) issue_loads(t + 1, (t + 1) & 1);
+    if (wave == 0 && t + 2 < ntp && t + 2 < t_end)
       fill_rowtab(t + 2, rowtab[t & 1], cur_seg, w.nseg, R, seg_start, seg_pref);
 
     f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
@@ -330,22 +373,37 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
     }
     __syncthreads();
   }
-  write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+  if (parts == 1) {
+    write_output(oacc, m_run, l_run, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
+    return;
+  }
+  merge_parts<QDT, kThreads, kStageOut>(a, sc, un, parts, oacc, m_run, l_run, w, qrow, L, H, g, merge_turn,
+                                        k_lds + wave * 32 * kOutPitch);
 }
 
 template <int QDT, int KDT, int VDT, int NQS, int NPS, int NVS>
 hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
-  // The split modes hold more pieces in LDS and registers: one 4-wave
-  // workgroup per CU, so a wave may hold 512 registers (no spills).
+  // 4-wave workgroups of 128 queries (the work plan's items).  The plain
+  // modes fit 256 registers per wave: two workgroups per CU.  The split modes
+  // hold more pieces in LDS and registers: one workgroup per CU, so a wave may
+  // hold 512 registers (no spills).
   constexpr bool kPlain = NQS <= 2 && NPS == 1 && NVS == 1;
-  constexpr int NW = kPlain ? 8 : 4;
+  constexpr int NW = 4;
   constexpr int MINB = kPlain ? 2 : 1;
   const int32_t n_qt = (a.cur_len + NW * 32 - 1) / (NW * 32);
   const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * n_qt;
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  AttnArgs b = a;
+  b.ws_cuts = 0;
+  if (a.workspace != nullptr && a.workspace_bytes > kCounterBytes) {
+    const int64_t by_records = (a.workspace_bytes - kCounterBytes) / (2LL * 66 * NW * 64 * 4);
+    b.ws_cuts = static_cast<int32_t>(by_records < kCounterBytes / 4 ? by_records : kCounterBytes / 4);
+  }
+  const int64_t grid = a.plan != nullptr ? a.plan_units : blocks;
+  if (grid <= 0) return hipSuccess;
   seg_attn_staged_kernel<QDT, KDT, VDT, NQS, NPS, NVS, NW, MINB>
-      <<<dim3(static_cast<uint32_t>(blocks)), NW * 64, 0, st>>>(a, s, n_qt);
+      <<<dim3(static_cast<uint32_t>(grid)), NW * 64, 0, st>>>(b, s, n_qt);
   return hipGetLastError();
 }
 

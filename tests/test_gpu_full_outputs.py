@@ -12,7 +12,9 @@ the reference CPU path restated) with the contract tolerances: out max-abs
 Workloads: the 2B final step (B=2, H=16, budget 0.1), the 8B-class final step
 (B=8, H=32) at budgets 0.05, 0.1, 0.2 and 1.0 (every prior token kept), and
 the skewed-ragged step (B=16, H=16, retained lengths log-uniform in
-[0, 6425]) -- every (b, h) of each.
+[0, 6425]) -- every (b, h) of each; and the 2B final step at the model's
+precision (fp32 q of norm 30, unit fp32 k, bf16 v, scale 1: the staged
+kernel) against the oracle in fp64.
 """
 
 from __future__ import annotations
@@ -31,12 +33,26 @@ pytestmark = pytest.mark.gpu
 ORACLE_WORKERS = 16
 
 
-def abi_attention(wl, device, *, workspace=True, planned=False):
+def model_precision(q, slab_k, ck):
+    """q, slab K and current K as the cosine-attention model passes them under
+    bf16 autocast: fp32, unit-norm k, q scaled to norm 30 (softmax scale 1).
+    Slab rows that no segment owns stay NaN."""
+    F = torch.nn.functional
+    return (F.normalize(q.float(), dim=-1) * 30.0, F.normalize(slab_k.float(), dim=-1),
+            F.normalize(ck.float(), dim=-1))
+
+
+def abi_attention(wl, device, *, workspace=True, planned=False, model=False):
     """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse
-    (``planned``: with the host work plan of its tables)."""
+    (``planned``: with the host work plan of its tables; ``model``: fp32 q/k at
+    the model's precision, scale 1, see model_precision)."""
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
+    scale = float(wl.softmax_scale)
+    if model:
+        q, slab_k, ck = model_precision(q, slab_k, ck)
+        scale = 1.0
     B, H, L, D = q.shape
     out = torch.full((B, L, H * D), float("nan"), dtype=q.dtype, device=device)
     lse = torch.full((B, H, L), float("nan"), dtype=torch.float32, device=device)
@@ -51,26 +67,32 @@ def abi_attention(wl, device, *, workspace=True, planned=False):
         q.data_ptr(), slab_k.data_ptr(), slab_v.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
         ck.data_ptr(), cv.data_ptr(), out.data_ptr(), lse.data_ptr(), B, H, L, int(slab_k.shape[1]),
         int(st.shape[1]), D, _lib.dtype_code(q.dtype), _lib.dtype_code(ck.dtype), _lib.dtype_code(cv.dtype), 0,
-        float(wl.softmax_scale), 0, 0, 0, plan.data_ptr() if plan is not None else None,
+        scale, 0, 0, 0, plan.data_ptr() if plan is not None else None,
         int(plan.shape[0]) if plan is not None else 0, ws.data_ptr() if ws is not None else None,
         int(ws.numel()) if ws is not None else 0, stream.cuda_stream)
     _lib.check(code)
     torch.cuda.synchronize(device)
-    return slab_k, slab_v, out, lse
+    return q, slab_k, slab_v, ck, out, lse
 
 
 def check_every_row(wl, device, **kw):
     B, H, L, D = wl.q.shape
     print(f"[full] {wl.name} budget={wl.budget} B={B} H={H} L={L} cap={wl.schedule.capacity} "
           f"R={sorted(set(wl.retained_rows()))[:3]}..{max(wl.retained_rows())}", flush=True)
-    slab_k, slab_v, out, lse = abi_attention(wl, device, **kw)
+    q, slab_k, slab_v, ck, out, lse = abi_attention(wl, device, **kw)
     o, l = to_np(out), to_np(lse)
     assert np.isfinite(o).all(), f"{wl.name}: rows left unwritten (NaN) in the output"
     assert np.isfinite(l).all(), f"{wl.name}: rows left unwritten (NaN) in the LSE"
     st, en, ct = (t.numpy() for t in wl.tables())
-    ref_out, ref_lse = oattn.flat_segmented_attention(
-        to_np(wl.q), to_np(slab_k), to_np(slab_v), st, en, ct, to_np(wl.cur_k), to_np(wl.cur_v),
-        wl.softmax_scale, workers=ORACLE_WORKERS)
+    if kw.get("model"):  # scores up to +-30: the oracle in fp64
+        ref_out, ref_lse = oattn.flat_segmented_attention(
+            to_np(q).astype(np.float64), to_np(slab_k).astype(np.float64), to_np(slab_v).astype(np.float64),
+            st, en, ct, to_np(ck).astype(np.float64), to_np(wl.cur_v).astype(np.float64), 1.0,
+            dtype=np.float64, workers=ORACLE_WORKERS)
+    else:
+        ref_out, ref_lse = oattn.flat_segmented_attention(
+            to_np(wl.q), to_np(slab_k), to_np(slab_v), st, en, ct, to_np(wl.cur_k), to_np(wl.cur_v),
+            wl.softmax_scale, workers=ORACLE_WORKERS)
     worst = (0.0, None)
     for b in range(B):
         for h in range(H):
@@ -120,3 +142,11 @@ def test_every_row_8b_class_planned(budget, device):
 
 def test_every_row_skewed_ragged_planned(device):
     check_every_row(W.config(5), device, planned=True)
+
+
+# The 2B final step at the model's precision (fp32 q/k through the staged
+# kernel), with and without the host work plan (cut items merged through the
+# workspace).
+@pytest.mark.parametrize("planned", [False, True])
+def test_every_row_2b_final_model_precision(planned, device):
+    check_every_row(W.config(2), device, planned=planned, model=True)
