@@ -103,15 +103,15 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *              tables itself), or a device copy of the plan that
  *              hkv_segmented_attention_plan built from host copies of these
  *              same tables, batch and cur_len: one workgroup per unit, no
- *              planning in the kernel.  Only the 16-bit kernel uses it (fp32 K
- *              or V, and the fp32 value mode, plan in the kernel).  A plan for
+ *              planning in the kernel (both kernels; a cut item's parts are
+ *              merged through the workspace, so cuts need one).  A plan for
  *              other tables gives wrong results but stays inside the tensors.
  *   workspace, workspace_bytes : NULL / 0, or device memory of at least
  *              hkv_segmented_attention_workspace_bytes(device) bytes whose
  *              first 64 KiB (per-item counters) are zero before its first
  *              use (the calls leave them zero again; the rest is scratch).
- *              With it, for 16-bit inputs, a launch with fewer than two
- *              rounds of (batch, head, 128-query tile) items per resident
+ *              With it and no plan, for 16-bit inputs, a launch with fewer
+ *              than two rounds of (batch, head, 128-query tile) items per resident
  *              workgroup slot (2 per CU) cuts some items into two halves of
  *              their key stream, merged through the workspace, so it fills
  *              whole rounds; without it every item is one workgroup.  Results
@@ -135,7 +135,6 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
-/*
  * Work plan of hkv_segmented_attention for host copies of its offset tables
  * (int32 seg_starts / seg_ends [heads, max_segments], seg_counts [heads]),
  * batch and cur_len, for a device with `slots` resident attention workgroups
@@ -145,8 +144,13 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
  * code on bad arguments.  Items (batch row, head, 128-query tile) are ordered
  * heaviest head first; when a launch has under four rounds of items per
  * slot, the heaviest items may be cut into two key-range parts chosen by
- * simulating the dispatch.  Host-only: no device call.  No counterpart in
- * the reference (its tables are the whole plan: the Triton grid walks them).
+ * simulating the dispatch, and with at least two rounds the items are dealt
+ * to the 8 XCDs (workgroup id % 8) in chunks of a (batch row, head)'s query
+ * tiles, each XCD's list padded to equal length with empty units (head -1,
+ * the workgroup leaves at once).  Unit: head, batch row * n_qt + query tile,
+ * first and end key tile, cut index (-1 = whole item), part (0 or 1), 0, 0.
+ * Host-only: no device call.  No counterpart in the reference (its tables
+ * are the whole plan: the Triton grid walks them).
  */
 int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
                                      const int32_t* seg_counts, int32_t heads, int32_t max_segments,
