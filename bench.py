@@ -45,8 +45,9 @@ prints one JSON line.
   RoPE table rows.
 * ``real_model``: the same final step as the cosine-attention model runs it
   under bf16 autocast: fp32 unit-norm k (slab and current), fp32 q scaled
-  by 30, bf16 v, softmax scale 1 (the staged kernel, split-bf16 q/k
-  products), with the nominal FLOP count; ``tf32_mode``: the same step with
+  by 30, bf16 v, softmax scale 1 (split-bf16 q/k products: the operator
+  writes K as split rows and runs the split-row kernel; the time includes
+  that split), with the nominal FLOP count; ``tf32_mode``: the same step with
   q and k in fp16 (TF32's significand, REAL_PRUNING_FUSED_QK_DOT_MODE=tf32).
 * ``measured_peaks``: what this device reaches on plain library work in the
   same run: a bf16 8192^3 GEMM (torch.matmul, hipBLASLt) in TFLOP/s and a
@@ -417,18 +418,27 @@ def time_real_model(device, steps=50, warmup=20):
 
     from heatkv_amd import workloads as W
 
+    from heatkv_amd import attention_queries_per_item
+    from heatkv_amd.segmented_cache import work_plans_enabled
+
     wl = W.config(2)
     kw = attention_call(wl, device)
+    plan16 = kw["work_plan"]
     kw["q"] = F.normalize(kw["q"].float(), dim=-1) * 30.0
     kw["current_k"] = F.normalize(kw["current_k"].float(), dim=-1)
     kw["persisted_k"] = F.normalize(kw["persisted_k"].float().nan_to_num(0.0), dim=-1)
     kw["softmax_scale"] = 1.0
+    qpi = attention_queries_per_item(torch.float32, torch.float32, kw["current_v"].dtype)
+    kw["work_plan"] = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len, queries_per_item=qpi)
+                       if work_plans_enabled(device) else None)
     ms, _ = time_attention(kw, device, steps, warmup)
     for name in ("q", "current_k", "persisted_k"):
         kw[name] = kw[name].half()
+    kw["work_plan"] = plan16
     ms16, _ = time_attention(kw, device, steps, warmup)
     flops = wl.attention_flops()
-    return {"what": "2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 (staged kernel)",
+    kernel = "split-row kernel, K split once per call" if qpi == 256 else "staged kernel"
+    return {"what": f"2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 ({kernel})",
             "ms_per_step": round(ms, 4), "tflops_nominal": round(flops / (ms * 1e-3) / 1e12, 1),
             "pct_of_bf16_peak_nominal": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2),
             "tf32_mode": {"what": "same step, q/k in fp16 (16-bit kernel)", "ms_per_step": round(ms16, 4),

@@ -7,6 +7,7 @@ descriptors) is computed on the host like the reference's.
 """
 
 from .real_pruning_fused_attention import (  # noqa: F401
+    attention_queries_per_item,
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
     segmented_attention_plan,

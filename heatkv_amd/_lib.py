@@ -24,6 +24,7 @@ HKV_ERR_LAUNCH = -3
 HKV_ERR_DEVICE = -4
 
 DTYPE_CODES = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
+DTYPE_SPLIT_ROWS = 4  # K only: fp32 rows as bf16 high parts then low parts (hkv_split_rows)
 
 # Leading bytes of the attention workspace that must be zero before a call
 # (the per-item counters; the partial records behind them are written before
@@ -61,7 +62,9 @@ SIGNATURES = {
          _c_i32, _c_p, _c_i32, _c_p],
     ),
     "hkv_segmented_attention_plan": (
-        _c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i32]),
+        _c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i32]),
+    "hkv_segmented_attention_item_shape": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
+    "hkv_split_rows": (_c_i32, [_c_p, _c_p, _c_i64, _c_p]),
     "hkv_segmented_attention_slots": (_c_i32, [_c_i32]),
     "hkv_segmented_attention_workspace_bytes": (_c_i64, [_c_i32]),
     "hkv_qkv_produce": (

@@ -165,11 +165,18 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
     return fail(HKV_ERR_INVALID_ARG, "batch and heads must be positive (got %d, %d)", batch, heads);
   if (heads > 1024)
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented supports at most 1024 heads (got %d)", heads);
-  if (elem_bytes(q_dtype) == 0 || elem_bytes(k_dtype) == 0 || elem_bytes(v_dtype) == 0)
+  const bool split_k = k_dtype == HKV_DTYPE_SPLIT_ROWS;
+  if (elem_bytes(q_dtype) == 0 || (elem_bytes(k_dtype) == 0 && !split_k) || elem_bytes(v_dtype) == 0)
     return fail(HKV_ERR_UNSUPPORTED,
                 "real_scale_fused_segmented supports only float16, bfloat16, or float32 tensors");
-  if (q_dtype != k_dtype)
+  if (split_k) {
+    if (q_dtype != HKV_DTYPE_F32 || elem_bytes(v_dtype) != 2 || qk_dot_mode == 2 || value_dot_mode == 2)
+      return fail(HKV_ERR_UNSUPPORTED,
+                  "split K rows take float32 q, 16-bit v and the default (or tf32) dot modes (got q %d, v %d, "
+                  "modes %d/%d)", q_dtype, v_dtype, qk_dot_mode, value_dot_mode);
+  } else if (q_dtype != k_dtype) {
     return fail(HKV_ERR_UNSUPPORTED, "q and k must share one dtype (got %d and %d)", q_dtype, k_dtype);
+  }
   if (out_dtype == 0) out_dtype = q_dtype;
   if (elem_bytes(out_dtype) == 0)
     return fail(HKV_ERR_UNSUPPORTED, "out_dtype must be 0 (q's dtype), float16, bfloat16 or float32 (got %d)",
@@ -329,11 +336,13 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
 
 int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
                                      const int32_t* seg_counts, int32_t heads, int32_t max_segments,
-                                     int64_t slab_capacity, int32_t batch, int32_t cur_len, int32_t slots,
-                                     int32_t* units, int32_t max_units) {
+                                     int64_t slab_capacity, int32_t batch, int32_t cur_len,
+                                     int32_t queries_per_item, int32_t slots, int32_t* units, int32_t max_units) {
   if (heads <= 0 || heads > 1024 || batch <= 0 || cur_len <= 0)
     return fail(HKV_ERR_INVALID_ARG, "heads in [1, 1024], batch and cur_len positive (got %d, %d, %d)", heads, batch,
                 cur_len);
+  if (queries_per_item != 128 && queries_per_item != 256)
+    return fail(HKV_ERR_INVALID_ARG, "queries_per_item must be 128 or 256 (got %d)", queries_per_item);
   if (max_segments < 0 || max_segments > hkv::kMaxSegments)
     return fail(HKV_ERR_UNSUPPORTED, "max_segments must be in [0, %d] (got %d)", hkv::kMaxSegments, max_segments);
   if (slab_capacity < 0 || slots < 0 || max_units < 0)
@@ -343,10 +352,40 @@ int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* s
   const int64_t items = static_cast<int64_t>(batch) * heads * ((cur_len + 127) / 128);
   if (items > 0x3fffffffLL / 2) return fail(HKV_ERR_UNSUPPORTED, "too many work items (%lld)", static_cast<long long>(items));
   const int32_t n = hkv::build_attention_plan(seg_starts, seg_ends, seg_counts, heads, max_segments, slab_capacity,
-                                              batch, cur_len, slots, units, max_units);
+                                              batch, cur_len, queries_per_item, slots, units, max_units);
   if (n < 0) return fail(HKV_ERR_INVALID_ARG, "the plan needs more than max_units = %d units", max_units);
   ok();
   return n;
+}
+
+int32_t hkv_segmented_attention_item_shape(int32_t q_dtype, int32_t k_dtype, int32_t v_dtype, int32_t heads,
+                                           int32_t qk_dot_mode, int32_t value_dot_mode, int32_t device,
+                                           int32_t* slots) {
+  hkv::AttnArgs a{};
+  a.q_dtype = q_dtype;
+  a.k_dtype = k_dtype;
+  a.v_dtype = v_dtype;
+  a.heads = heads;
+  a.qk_dot_mode = qk_dot_mode;
+  a.value_dot_mode = value_dot_mode;
+  const int32_t q = hkv::attention_item_queries(a);
+  if (slots != nullptr) {
+    const int32_t s = hkv::split_slots(device);
+    if (s <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
+    *slots = q == 128 ? s : s / 2;  // 2 workgroups per CU, or 1 for the 256-query kernel
+  }
+  ok();
+  return q;
+}
+
+int32_t hkv_split_rows(const float* src, void* dst, int64_t rows, void* stream) {
+  if (rows < 0) return fail(HKV_ERR_INVALID_ARG, "rows must be >= 0 (got %lld)", static_cast<long long>(rows));
+  if (rows > 0 && (!src || !dst)) return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) != 0)
+    return fail(HKV_ERR_INVALID_ARG, "src and dst must be 16-byte aligned");
+  const hipError_t e = hkv::launch_split_rows(src, dst, rows, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HKV_ERR_LAUNCH, "split rows launch failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 int32_t hkv_segmented_attention_slots(int32_t device) {

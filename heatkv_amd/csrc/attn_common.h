@@ -863,6 +863,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
 
 hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);
 hipError_t launch_attention_staged(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);
+hipError_t launch_attention_split(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);
 bool attention_direct_supported(const AttnArgs& a);
 
 }  // namespace hkv

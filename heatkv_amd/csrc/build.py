@@ -15,8 +15,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ("abi.hip", "pack.hip", "produce.hip", "plan.hip", "seg_attn.hip", "seg_attn_staged.hip",
-           "seg_attn_direct.hip")
+SOURCES = ("abi.hip", "pack.hip", "produce.hip", "plan.hip", "seg_attn.hip", "seg_attn_split.hip",
+           "seg_attn_staged.hip", "seg_attn_direct.hip")
 ARCH = "gfx950"
 LIB = os.path.join(PKG, "libheatkv.so")
 

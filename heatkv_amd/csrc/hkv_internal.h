@@ -29,7 +29,9 @@ struct PackArgs {
 
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
-enum Dtype : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3 };
+// kSplitRows: fp32 K rows stored as split rows (128 bf16 high parts, then
+// 128 bf16 low parts; 512 bytes a row), the split kernel's K format.
+enum Dtype : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3, kSplitRows = 4 };
 
 // Dot modes of the reference's REAL_PRUNING_FUSED_QK_DOT_MODE /
 // REAL_PRUNING_FUSED_VALUE_DOT_MODE knobs (0 = default, 1 = TF32 (QK only),
@@ -70,8 +72,14 @@ struct AttnArgs {
 // (b * n_qt + qt), key tiles [t0, t1), cut item (-1 = whole) and part.
 constexpr int kPlanInts = 8;
 int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
-                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t slots,
+                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t bm, int32_t slots,
                              int32_t* out, int32_t max_units);
+
+// The split-row kernel (seg_attn_split.hip): fp32 q, kSplitRows K, 16-bit V
+// at the default dot modes; 256-query items, one workgroup per CU.
+bool attention_split_supported(const AttnArgs& a);
+int32_t attention_item_queries(const AttnArgs& a);
+hipError_t launch_split_rows(const float* src, void* dst, int64_t rows, hipStream_t stream);
 
 constexpr int kMaxSegments = 256;
 

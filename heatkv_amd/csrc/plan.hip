@@ -7,8 +7,8 @@
 // order once on the host from its copy of the tables and pass it with every
 // call (as the reference uploads its offset tables once per layer and target,
 // enable_real_pruning_fast.py:592-608).  A plan is a list of units, one per
-// workgroup in dispatch order: a whole item (b, h, 128-query tile) or one of
-// the two key-range parts of a cut item.
+// workgroup in dispatch order: a whole item (b, h, query tile of the
+// kernel's bm queries) or one of the two key-range parts of a cut item.
 //
 // Choosing the cuts.  The hardware dispatches workgroups in id order to
 // whatever slot frees first, i.e. list scheduling.  The plan simulates it
@@ -45,7 +45,6 @@ namespace hkv {
 namespace {
 
 constexpr int kPlanBN = 64;            // keys per tile
-constexpr int kPlanBM = 128;           // queries per item
 constexpr int kPlanMinPartTiles = 8;   // a part must have this many key tiles
 constexpr double kUnitOverTiles = 1.5;  // start-up of a workgroup, in key-tile times
 constexpr double kPartOverTiles = 4.0;  // record publish + merge of a part
@@ -180,9 +179,9 @@ bool deal_enabled() {
 }  // namespace
 
 int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
-                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t slots,
+                             int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t bm, int32_t slots,
                              int32_t* out, int32_t max_units) {
-  const int32_t n_qt = (L + kPlanBM - 1) / kPlanBM;
+  const int32_t n_qt = (L + bm - 1) / bm;
   const int32_t ntc = (L + kPlanBN - 1) / kPlanBN;
   std::vector<int64_t> rows(H, 0);
   for (int32_t h = 0; h < H; ++h) {

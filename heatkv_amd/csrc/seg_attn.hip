@@ -1,4 +1,5 @@
-// Segmented attention launch: picks the direct-to-LDS kernel for 16-bit K/V
+// Segmented attention launch: the split-row kernel for K in split rows
+// (seg_attn_split.hip), the direct-to-LDS kernel for 16-bit K/V
 // (seg_attn_direct.hip) and the register-staged kernel otherwise
 // (seg_attn_staged.hip).  HKV_ATTN_PATH=staged (read once) forces the staged
 // kernel, for comparisons.
@@ -20,12 +21,14 @@ bool force_staged() {
 }  // namespace
 
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream) {
-  if (a.heads > attn::kMaxHeads || a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
+  if (a.heads > attn::kMaxHeads) return hipErrorInvalidValue;
   attn::Scalars s;
   const float scale_abs = a.softmax_scale < 0.f ? -a.softmax_scale : a.softmax_scale;
   s.c = fmaxf(scale_abs * attn::kLog2e, attn::kMinC);
   s.thresh = attn::kRescaleLog2 / s.c;
   s.q_sign = a.softmax_scale < 0.f ? 0x80008000u : 0u;
+  if (a.k_dtype == kSplitRows) return launch_attention_split(a, s, stream);
+  if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
   if (!force_staged() && attention_direct_supported(a)) return launch_attention_direct(a, s, stream);
   return launch_attention_staged(a, s, stream);
 }

@@ -77,15 +77,19 @@ PLAN_INTS = 8
 
 
 def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, batch_size: int,
-                             current_len: int, capacity: int, device=None, slots: Optional[int] = None):
+                             current_len: int, capacity: int, device=None, slots: Optional[int] = None,
+                             queries_per_item: int = 128):
     """Work plan of :func:`fused_real_pruning_flat_segmented_attention` for
     host copies of its offset tables (``[H, S]``, ``[H]``; torch CPU tensors
     or numpy arrays), ``batch_size``, ``current_len`` and slab ``capacity``:
     an int32 tensor ``[units, 8]`` on ``device`` (host when None) to pass as
-    ``work_plan`` with every call on those tables.  Built on the host by
+    ``work_plan`` with every call on those tables.  ``queries_per_item`` is
+    the kernel's (:func:`attention_queries_per_item`: 128, or 256 for fp32
+    q/k with 16-bit v); the tensor carries it as ``hkv_queries_per_item`` and
+    the operator checks it.  Built on the host by
     ``hkv_segmented_attention_plan``; ``slots`` defaults to the device's
-    resident attention workgroups.  No counterpart in the reference, whose
-    Triton grid walks the tables directly."""
+    resident attention workgroups for that kernel.  No counterpart in the
+    reference, whose Triton grid walks the tables directly."""
     import numpy as np
 
     def host(t):
@@ -104,9 +108,10 @@ def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, ba
         slots = int(lib.hkv_segmented_attention_slots(idx))
         if slots < 0:
             _lib.check(slots)
+        slots = slots * 128 // int(queries_per_item)  # one 256-query workgroup per CU
     H, S = st.shape
     args = (st.ctypes.data, en.ctypes.data, ct.ctypes.data, H, S, int(capacity), int(batch_size),
-            int(current_len), int(slots))
+            int(current_len), int(queries_per_item), int(slots))
     n = int(lib.hkv_segmented_attention_plan(*args, None, 0))
     if n < 0:
         _lib.check(n)
@@ -115,7 +120,40 @@ def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, ba
     if n < 0:
         _lib.check(n)
     out = torch.from_numpy(plan[:n].copy())
-    return out.to(device) if device is not None else out
+    if device is not None:
+        out = out.to(device)
+    out.hkv_queries_per_item = int(queries_per_item)
+    return out
+
+
+def _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int) -> bool:
+    """fp32 q/k with 16-bit v at dot modes other than fp32 run the split-row
+    kernel: K is first written as split rows (hkv_split_rows).  HKV_ATTN_SPLIT_ROWS=0
+    keeps them on the register-staged kernel (for comparisons)."""
+    if os.environ.get("HKV_ATTN_SPLIT_ROWS", "1").strip().lower() in {"0", "false", "no", "off"}:
+        return False
+    return (q_dtype == torch.float32 and k_dtype == torch.float32 and v_dtype in (torch.float16, torch.bfloat16)
+            and qk_mode != 2 and value_mode != 2)
+
+
+def attention_queries_per_item(q_dtype, k_dtype, v_dtype) -> int:
+    """Queries per work item of the kernel that :func:`fused_real_pruning_flat_segmented_attention`
+    runs for these dtypes at the current dot-mode knobs (the ``queries_per_item``
+    of :func:`segmented_attention_plan`): 256 for the split-row kernel, else 128."""
+    split = _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(), _fused_value_dot_mode_id())
+    return 256 if split else 128
+
+
+def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
+    """fp32 ``[..., 128]`` rows as split rows ``[..., 256]`` bf16 (128 high
+    parts, then 128 low parts), by the HIP kernel ``hkv_split_rows``."""
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    out = torch.empty(tuple(t.shape[:-1]) + (2 * t.shape[-1],), device=t.device, dtype=torch.bfloat16)
+    rows = t.numel() // t.shape[-1]
+    if rows > 0:
+        _lib.check(_lib.load().hkv_split_rows(t.data_ptr(), out.data_ptr(), rows, stream.cuda_stream))
+    return out
 
 
 def pack_flat_segments_kv(
@@ -311,14 +349,26 @@ def fused_real_pruning_flat_segmented_attention(
         if return_lse
         else None
     )
+    split = _split_rows_path(q.dtype, current_k.dtype, current_v.dtype, qk_mode, value_mode)
     if work_plan is not None:
         if (work_plan.dtype != torch.int32 or work_plan.ndim != 2 or work_plan.shape[1] != PLAN_INTS
                 or not work_plan.is_contiguous()):
             raise ValueError(f"work_plan must be a contiguous int32 tensor [units, {PLAN_INTS}]")
         if work_plan.device != q.device:
             raise ValueError("work_plan must be on the same device as q")
+        want = 256 if split else 128
+        have = getattr(work_plan, "hkv_queries_per_item", want)
+        if have != want:
+            raise ValueError(f"work_plan was built for {have}-query items; this call's kernel takes {want} "
+                             "(segmented_attention_plan(..., queries_per_item=attention_queries_per_item(...)))")
     stream = torch.cuda.current_stream(q.device)
     ws = _lib.attention_workspace(q.device, stream)
+    k_code = _lib.dtype_code(current_k.dtype)
+    if split:
+        # fp32 K as split rows for the split-row kernel (the q split happens in it)
+        persisted_k = _split_rows(persisted_k, stream)
+        current_k = _split_rows(current_k, stream)
+        k_code = _lib.DTYPE_SPLIT_ROWS
     code = _lib.load().hkv_segmented_attention(
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
         segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
@@ -326,7 +376,7 @@ def fused_real_pruning_flat_segmented_attention(
         lse.data_ptr() if lse is not None else None,
         batch_size, num_heads, current_len,
         int(persisted_k.shape[1]), int(segment_starts.shape[1]), head_dim,
-        _lib.dtype_code(q.dtype), _lib.dtype_code(current_k.dtype), _lib.dtype_code(current_v.dtype),
+        _lib.dtype_code(q.dtype), k_code, _lib.dtype_code(current_v.dtype),
         _lib.dtype_code(out_dtype), float(softmax_scale), 1 if softmax_mode == "exp2" else 0, qk_mode, value_mode,
         work_plan.data_ptr() if work_plan is not None else None,
         int(work_plan.shape[0]) if work_plan is not None else 0,

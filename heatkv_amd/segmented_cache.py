@@ -34,6 +34,7 @@ import torch
 
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
+    attention_queries_per_item,
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
     segmented_attention_plan,
@@ -166,32 +167,33 @@ class SegmentedLayerCache:
 
     # ------------------------------------------------------------------ attention
 
-    def _dense_tables(self, heads: int, T: int, device, batch: int, L: int):
+    def _dense_tables(self, heads: int, T: int, device, batch: int, L: int, qpi: int = 128):
         """Offset tables that present a dense cache ``[B, H, T, D]`` as a slab
-        ``[B, H*T, D]``, and their work plan for ``batch`` x ``L`` queries."""
-        key = (heads, T, str(device), batch, L)
+        ``[B, H*T, D]``, and their work plan for ``batch`` x ``L`` queries
+        (``qpi``: the kernel's queries per item)."""
+        key = (heads, T, str(device), batch, L, qpi)
         hit = self._tables_by_len.get(key)
         if hit is None:
             starts = (torch.arange(heads, dtype=torch.int32) * T).reshape(heads, 1)
             ends = starts + T
             counts = torch.ones((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
-                                             capacity=heads * T, device=device)
+                                             capacity=heads * T, device=device, queries_per_item=qpi)
                     if work_plans_enabled(device) and not _capturing() else None)
             hit = (starts.to(device), ends.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
 
-    def _empty_tables(self, heads: int, device, batch: int, L: int):
+    def _empty_tables(self, heads: int, device, batch: int, L: int, qpi: int = 128):
         """Tables with no segment (attention over the current scale only) and
         their work plan, made once."""
-        key = ("empty", heads, str(device), batch, L)
+        key = ("empty", heads, str(device), batch, L, qpi)
         hit = self._tables_by_len.get(key)
         if hit is None:
             empty = torch.zeros((heads, 0), dtype=torch.int32)
             counts = torch.zeros((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(empty, empty, counts, batch_size=batch, current_len=L, capacity=0,
-                                             device=device)
+                                             device=device, queries_per_item=qpi)
                     if work_plans_enabled(device) and not _capturing() else None)
             hit = (empty.to(device), empty.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
@@ -199,12 +201,13 @@ class SegmentedLayerCache:
 
     def _attend_dense(self, q, k, v, scale, mode, out_dtype=None):
         B, H, L, D = q.shape
+        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype)
         if self.cached_k is None or self.logical_len == 0:
-            tables = self._empty_tables(H, q.device, B, L)
+            tables = self._empty_tables(H, q.device, B, L, qpi)
             slab_k = slab_v = None
         else:
             T = self.cached_k.shape[2]
-            tables = self._dense_tables(H, T, q.device, B, L)
+            tables = self._dense_tables(H, T, q.device, B, L, qpi)
             slab_k = self.cached_k.reshape(B, H * T, D)
             slab_v = self.cached_v.reshape(B, H * T, D)
         return fused_real_pruning_flat_segmented_attention(
@@ -282,7 +285,9 @@ class SegmentedLayerCache:
                     self._activate_from_dense(self.cached_k, self.cached_v, scale_ind)
                 starts, ends, counts = self.schedule.device_tables(scale_ind, q.device)
                 plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]),
-                                                       build=not _capturing())
+                                                       build=not _capturing(),
+                                                       queries_per_item=attention_queries_per_item(
+                                                           q.dtype, k.dtype, v.dtype))
                         if work_plans_enabled(q.device) else None)
             with prof.phase("attention"):
                 out = fused_real_pruning_flat_segmented_attention(

@@ -133,20 +133,22 @@ class SlabSchedule:
             self._device_cache[key] = hit
         return hit
 
-    def device_work_plan(self, target: int, device, batch: int, cur_len: int, *,
-                         build: bool = True) -> Optional[torch.Tensor]:
+    def device_work_plan(self, target: int, device, batch: int, cur_len: int, *, build: bool = True,
+                         queries_per_item: int = 128) -> Optional[torch.Tensor]:
         """Attention work plan of ``target``'s tables for ``batch`` rows of
-        ``cur_len`` queries on ``device`` (segmented_attention_plan), built on
-        the host and moved once, cached.  With ``build=False`` only a plan
-        already made is returned (None otherwise)."""
+        ``cur_len`` queries on ``device`` (segmented_attention_plan) for a
+        kernel of ``queries_per_item``-query items, built on the host and
+        moved once, cached.  With ``build=False`` only a plan already made is
+        returned (None otherwise)."""
         from .real_pruning_fused_attention import segmented_attention_plan
 
-        key = ("work_plan", str(device), int(target), int(batch), int(cur_len))
+        key = ("work_plan", str(device), int(target), int(batch), int(cur_len), int(queries_per_item))
         hit = self._device_cache.get(key)
         if hit is None and build:
             st, en, ct = self.tables[int(target)]
             hit = segmented_attention_plan(st, en, ct, batch_size=batch, current_len=cur_len,
-                                           capacity=self.capacity, device=device)
+                                           capacity=self.capacity, device=device,
+                                           queries_per_item=queries_per_item)
             self._device_cache[key] = hit
         return hit
 

@@ -27,6 +27,12 @@ extern "C" {
 #define HKV_DTYPE_F16 1
 #define HKV_DTYPE_BF16 2
 #define HKV_DTYPE_F32 3
+/* K only: fp32 rows stored as split rows, 128 bf16 high parts then 128 bf16
+ * low parts per row (hi = x rounded to bf16, lo = (x - hi) rounded to bf16;
+ * 512 bytes a row, written by hkv_split_rows).  With float32 q, 16-bit v and
+ * the default (or tf32) dot modes the attention then runs its split-row
+ * kernel.  No counterpart in the reference. */
+#define HKV_DTYPE_SPLIT_ROWS 4
 
 /* Library version, (major << 16) | (minor << 8) | patch. Loader check. */
 int32_t hkv_version(void);
@@ -85,7 +91,12 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
  *          nearest even, what a later cast of an fp32 output would give)
  *   lse  : NULL, or float32 [batch, heads, cur_len] natural-log log-sum-exp
  *          of the scaled scores (not produced by the reference kernel)
- *   *_dtype : HKV_DTYPE_*; slab and current K share k_dtype, V share v_dtype
+ *   *_dtype : HKV_DTYPE_*; slab and current K share k_dtype, V share v_dtype;
+ *              k_dtype HKV_DTYPE_SPLIT_ROWS needs q float32, v 16-bit and
+ *              dot modes other than 2 (its rows are 512 bytes: slab_k is
+ *              [batch, slab_capacity, 256] and cur_k [batch, heads, cur_len,
+ *              256] of bf16); the work plan's items are then 256 queries
+ *              (hkv_segmented_attention_item_shape)
  *   use_exp2 : the reference's softmax_mode ("exp" = 0, "exp2" = 1); both give
  *              the same mathematical result and this kernel always evaluates
  *              exp2 with scale*log2(e) folded in.
@@ -137,8 +148,9 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
 /*
  * Work plan of hkv_segmented_attention for host copies of its offset tables
  * (int32 seg_starts / seg_ends [heads, max_segments], seg_counts [heads]),
- * batch and cur_len, for a device with `slots` resident attention workgroups
- * (hkv_segmented_attention_slots; 0 = cut nothing): writes plan units of 8
+ * batch and cur_len, for items of `queries_per_item` queries (128, or 256
+ * for split K rows) and a device with `slots` resident attention workgroups
+ * (hkv_segmented_attention_item_shape; 0 = cut nothing): writes plan units of 8
  * int32 each into `units` (host memory, room for max_units) and returns
  * their count, or only the count when `units` is NULL; a negative HKV_ERR_*
  * code on bad arguments.  Items (batch row, head, 128-query tile) are ordered
@@ -154,8 +166,27 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
  */
 int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
                                      const int32_t* seg_counts, int32_t heads, int32_t max_segments,
-                                     int64_t slab_capacity, int32_t batch, int32_t cur_len, int32_t slots,
-                                     int32_t* units, int32_t max_units);
+                                     int64_t slab_capacity, int32_t batch, int32_t cur_len,
+                                     int32_t queries_per_item, int32_t slots, int32_t* units, int32_t max_units);
+
+/*
+ * Item shape of hkv_segmented_attention for these dtypes and dot modes:
+ * returns the queries per work item (128, or 256 for split K rows), and
+ * writes the device's resident attention workgroups for that kernel to
+ * *slots when slots is not NULL (the `queries_per_item` and `slots` of
+ * hkv_segmented_attention_plan); a negative HKV_ERR_* code when the device
+ * cannot be queried.  No counterpart in the reference.
+ */
+int32_t hkv_segmented_attention_item_shape(int32_t q_dtype, int32_t k_dtype, int32_t v_dtype, int32_t heads,
+                                           int32_t qk_dot_mode, int32_t value_dot_mode, int32_t device,
+                                           int32_t* slots);
+
+/*
+ * fp32 rows (`rows` x 128 contiguous, 16-byte aligned) to split rows at dst
+ * (`rows` x 512 bytes, see HKV_DTYPE_SPLIT_ROWS), enqueued on `stream`.  No
+ * counterpart in the reference: its Triton dot takes fp32 K as it is.
+ */
+int32_t hkv_split_rows(const float* src, void* dst, int64_t rows, void* stream);
 
 /* Resident attention workgroups of `device` (2 per CU), the `slots` of
  * hkv_segmented_attention_plan; a negative HKV_ERR_* code when the device

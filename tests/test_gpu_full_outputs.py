@@ -42,10 +42,11 @@ def model_precision(q, slab_k, ck):
             F.normalize(ck.float(), dim=-1))
 
 
-def abi_attention(wl, device, *, workspace=True, planned=False, model=False):
+def abi_attention(wl, device, *, workspace=True, planned=False, model=False, split_rows=False):
     """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse
     (``planned``: with the host work plan of its tables; ``model``: fp32 q/k at
-    the model's precision, scale 1, see model_precision)."""
+    the model's precision, scale 1, see model_precision; ``split_rows``: K
+    passed as split rows, the split-row kernel with 256-query items)."""
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
@@ -61,12 +62,21 @@ def abi_attention(wl, device, *, workspace=True, planned=False, model=False):
     if planned:
         hst, hen, hct = wl.tables()
         plan = segmented_attention_plan(hst, hen, hct, batch_size=B, current_len=L,
-                                        capacity=wl.schedule.capacity, device=device)
+                                        capacity=wl.schedule.capacity, device=device,
+                                        queries_per_item=256 if split_rows else 128)
     stream = torch.cuda.current_stream(device)
+    k_args = (slab_k, ck, _lib.dtype_code(ck.dtype))
+    if split_rows:
+        sk2 = torch.empty(tuple(slab_k.shape[:-1]) + (256,), dtype=torch.bfloat16, device=device)
+        ck2 = torch.empty(tuple(ck.shape[:-1]) + (256,), dtype=torch.bfloat16, device=device)
+        for src, dst in ((slab_k.contiguous(), sk2), (ck.contiguous(), ck2)):
+            _lib.check(_lib.load().hkv_split_rows(src.data_ptr(), dst.data_ptr(), src.numel() // 128,
+                                                  stream.cuda_stream))
+        k_args = (sk2, ck2, _lib.DTYPE_SPLIT_ROWS)
     code = _lib.load().hkv_segmented_attention(
-        q.data_ptr(), slab_k.data_ptr(), slab_v.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
-        ck.data_ptr(), cv.data_ptr(), out.data_ptr(), lse.data_ptr(), B, H, L, int(slab_k.shape[1]),
-        int(st.shape[1]), D, _lib.dtype_code(q.dtype), _lib.dtype_code(ck.dtype), _lib.dtype_code(cv.dtype), 0,
+        q.data_ptr(), k_args[0].data_ptr(), slab_v.data_ptr(), st.data_ptr(), en.data_ptr(), ct.data_ptr(),
+        k_args[1].data_ptr(), cv.data_ptr(), out.data_ptr(), lse.data_ptr(), B, H, L, int(slab_k.shape[1]),
+        int(st.shape[1]), D, _lib.dtype_code(q.dtype), k_args[2], _lib.dtype_code(cv.dtype), 0,
         scale, 0, 0, 0, plan.data_ptr() if plan is not None else None,
         int(plan.shape[0]) if plan is not None else 0, ws.data_ptr() if ws is not None else None,
         int(ws.numel()) if ws is not None else 0, stream.cuda_stream)
@@ -144,9 +154,10 @@ def test_every_row_skewed_ragged_planned(device):
     check_every_row(W.config(5), device, planned=True)
 
 
-# The 2B final step at the model's precision (fp32 q/k through the staged
-# kernel), with and without the host work plan (cut items merged through the
-# workspace).
+# The 2B final step at the model's precision: fp32 q/k through the staged
+# kernel, and with K as split rows through the split-row kernel; with and
+# without the host work plan (cut items merged through the workspace).
 @pytest.mark.parametrize("planned", [False, True])
-def test_every_row_2b_final_model_precision(planned, device):
-    check_every_row(W.config(2), device, planned=planned, model=True)
+@pytest.mark.parametrize("split_rows", [False, True])
+def test_every_row_2b_final_model_precision(planned, split_rows, device):
+    check_every_row(W.config(2), device, planned=planned, model=True, split_rows=split_rows)

@@ -423,3 +423,74 @@ def test_attention_random_shapes_planned(seed, device, monkeypatch):
     ref_out, ref_lse = oattn.flat_segmented_attention(
         to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale, workers=16)
     assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse, what=f"planned seed {seed}")
+
+
+@pytest.mark.parametrize("seed", list(range(70, 76)))
+def test_attention_random_shapes_split_rows(seed, device, monkeypatch):
+    """fp32 q/k with bf16 v (the split-row kernel: 256-query items, K written
+    as split rows per call) on random shapes, with the host work plan of
+    256-query items (every other seed without the workspace: cut units run
+    whole) and without a plan, against the oracle; scores of O(10) (q and k
+    of norm ~sqrt(128) / 3.5) so the split's ~16 bits matter."""
+    from heatkv_amd import attention_queries_per_item, segmented_attention_plan
+
+    g = torch.Generator().manual_seed(seed)
+
+    def pick(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    B, H, L, cap, S = pick(1, 3), pick(1, 24), pick(1, 2300), pick(0, 4000), pick(0, 30)
+    if cap == 0:
+        S = 0
+    monkeypatch.setenv("HKV_ATTN_SPLIT", "1" if seed % 2 else "0")
+    qpi = attention_queries_per_item(torch.float32, torch.float32, torch.bfloat16)
+    assert qpi == 256
+    print(f"[attn] split rows random shape seed={seed} B={B} H={H} L={L} cap={cap} S={S}", flush=True)
+    q, sk, sv, tables, ck, cv = _random_case(seed, B, H, L, cap, S, dtype=torch.float32, kdtype=torch.float32,
+                                             vdtype=torch.bfloat16)
+    scale = 0.3
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q), to_np(sk), to_np(sv), *(t.numpy() for t in tables), to_np(ck), to_np(cv), scale, workers=16)
+    plan = segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device,
+                                    queries_per_item=qpi)
+    for wp in (plan, None):
+        out, lse = _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=wp)
+        assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse,
+                                what=f"split rows seed {seed} plan={wp is not None}")
+    # a plan of 128-query items does not fit the split-row kernel
+    if L > 0:
+        plan128 = segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device)
+        with pytest.raises(ValueError, match="128-query items"):
+            _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan128)
+
+
+def test_split_rows_bit_exact(device):
+    """hkv_split_rows against the split restated in numpy: hi = x rounded to
+    bf16 (nearest even), lo = (x - hi) rounded to bf16 (x - hi is exact in
+    fp32), including values that round up across a power of two, ties, zeros,
+    signs and magnitudes from 1e-30 to 1e38 (no subnormals: their rounding
+    follows the device's denormal mode)."""
+    from heatkv_amd import _lib
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((333, 128), generator=g) * torch.logspace(-30, 30, 128).view(1, 128)
+    x[0, :8] = torch.tensor([0.0, -0.0, 1.0, -1.0, 1.00390625, 1.0 + 2 ** -8 + 2 ** -20, 3.0, -3.0])
+    x[1, :4] = torch.tensor([255.99999, 65535.9, -1.5e38, 1e-30])
+    xd = x.to(device)
+    out = torch.empty((333, 256), dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.current_stream(device)
+    _lib.check(_lib.load().hkv_split_rows(xd.data_ptr(), out.data_ptr(), 333, stream.cuda_stream))
+    torch.cuda.synchronize(device)
+    got = out.cpu().view(torch.int16).numpy().astype(np.uint16)
+
+    def bf16_rne(a):  # float32 numpy -> bf16 bits, round to nearest even
+        u = a.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        return r
+
+    xn = x.numpy().astype(np.float32)
+    hi = bf16_rne(xn)
+    hi_f = (hi.astype(np.uint32) << 16).view(np.float32)
+    lo = bf16_rne((xn - hi_f).astype(np.float32))
+    assert np.array_equal(got[:, :128], hi)
+    assert np.array_equal(got[:, 128:], lo)
