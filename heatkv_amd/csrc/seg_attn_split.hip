@@ -15,17 +15,19 @@
 //  * A 64-key tile moves global -> LDS with buffer_load_dwordx4 ... lds in
 //    MFMA-operand order: the hi plane and the lo plane of K (16 KiB each, the
 //    16-bit kernel's K block order) and V (16 KiB, the 16-bit kernel's V
-//    order, read with ds_read_b64_tr_b16).  Two stages: 96 KiB.
+//    order, read with ds_read_b64_tr_b16).  K has two stages, V three slots:
+//    112 KiB.
 //  * The software pipeline runs on 32-key halves: half j+1's 24 QK MFMAs
 //    (8 k-steps x 3 products) are issued while the VALU turns half j's
 //    scores into P, then half j's 8 PV MFMAs while the VALU takes half j+1's
 //    row max.  Two S halves of 16 registers each, so both q pieces (64
 //    registers) and O (64) fit 256 registers per wave.
 //  * K of tile T is read by the half steps 2T - 1 and 2T, V of tile T by 2T
-//    and 2T + 1, so K runs half a tile ahead of V: step 2T + 1 issues K(T + 2)
-//    (after a barrier that retires every read of K(T)) and step 2T issues
-//    V(T + 1) (retiring V(T - 1)); each DMA is issued two half steps before
-//    its first use.  One barrier per half step.
+//    and 2T + 1.  Step 2T + 1 waits for tile T + 1 (issued two half steps
+//    earlier), passes the tile's one barrier, which retires every read of
+//    K(T) and V(T - 1), and issues K and V of tile T + 2 into their places:
+//    each tile lands at least two half steps before its first use, and the
+//    even half steps neither wait nor synchronize.
 // Semantics as the other attention kernels (attn_common.h): online softmax in
 // the exp2 domain with the lazy rescale, P rounded to V's type, current-scale
 // tiles first, then the retained prior rows through the row tables.
@@ -42,7 +44,9 @@ constexpr int kSW = 8;                           // waves per workgroup
 constexpr int kSThreads = kSW * 64;
 constexpr int kSBM = kSW * 32;                   // queries per item
 constexpr int kSPlane = kBN * kD * 2;            // 16 KiB: one plane of a K tile
-constexpr int kSStage = 3 * kSPlane;             // K hi, K lo, V
+constexpr int kSKStage = 2 * kSPlane;            // K hi and lo planes of a tile
+constexpr int kSVBase = 2 * kSKStage;            // V slots after the two K stages
+constexpr int kSRing = kSVBase + 3 * kSPlane;    // 2 K stages + 3 V slots: 112 KiB
 constexpr int kSRowBytes = 2 * kD * 2;           // a split K row
 constexpr int kVRowBytes = kD * 2;               // a 16-bit V row
 constexpr int32_t kPastEnd = static_cast<int32_t>(0x80000000u);
@@ -140,12 +144,12 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   constexpr int kThreads = kSThreads;
   constexpr int kBM = kSBM;
   constexpr int MV = VDT;
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * kSStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kSRing];
   __shared__ __attribute__((aligned(16))) int32_t rowtab[3][kBN];
   __shared__ int32_t seg_start[kMaxSegments];
   __shared__ int32_t seg_pref[kMaxSegments + 1];
   __shared__ int32_t merge_turn;
-  static_assert(2 * kSStage >= kSW * 32 * kOutPitch, "output staging fits the ring");
+  static_assert(kSRing >= kSW * 32 * kOutPitch, "output staging fits the ring");
 
   const int64_t cap = a.slab_capacity;
   const int H = a.heads;
@@ -183,7 +187,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
     w = plan_work<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, H, a.max_segments, a.batch, n_qt,
                             head_rows, head_rows + kMaxHeads, seg_start, seg_pref,
                             static_cast<int32_t>(blockIdx.x), head_rows + 2 * kMaxHeads,
-                            2 * kSStage / 4 - 2 * kMaxHeads);
+                            kSRing / 4 - 2 * kMaxHeads);
   }
   const int32_t R = w.R;
   const int32_t ntc = (L + kBN - 1) / kBN;
@@ -235,7 +239,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   const uint32_t ring_lds = lds_address(ring);
 
   auto issue_k = [&](int T) {
-    const uint32_t dst = ring_lds + (T & 1) * kSStage + wave * 4 * 1024;
+    const uint32_t dst = ring_lds + (T & 1) * kSKStage + wave * 4 * 1024;
     if (T < ntc) {
       const uint32_t skip = static_cast<uint32_t>(T) * (kBN * kSRowBytes);
       const u32x4_t d = make_desc(k_cur + skip, static_cast<uint32_t>(L) * kSRowBytes - skip);
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
     }
   };
   auto issue_v = [&](int T) {
-    const uint32_t dst = ring_lds + (T & 1) * kSStage + 2 * kSPlane + wave * 2 * 1024;
+    const uint32_t dst = ring_lds + kSVBase + (T % 3) * kSPlane + wave * 2 * 1024;
     if (T < ntc) {
       const uint32_t skip = static_cast<uint32_t>(T) * (kBN * kVRowBytes);
       const u32x4_t d = make_desc(v_cur + skip, static_cast<uint32_t>(L) * kVRowBytes - skip);
@@ -289,7 +293,10 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   __syncthreads();
   issue_k(tb);
   issue_v(tb);
-  if (tb + 1 < te) issue_k(tb + 1);
+  if (tb + 1 < te) {
+    issue_k(tb + 1);
+    issue_v(tb + 1);
+  }
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     qh[ks] ^= sc.q_sign;
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
 
   // S^T of half j (keys 32 (j & 1) .. of tile j >> 1) from its stage
   auto qk = [&](f32x16_t& s, int j) {
-    const uint8_t* kst = ring + ((j >> 1) & 1) * kSStage + (j & 1) * 8 * 1024 + lane * 16;
+    const uint8_t* kst = ring + ((j >> 1) & 1) * kSKStage + (j & 1) * 8 * 1024 + lane * 16;
     s = f32x16_t{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   };
   // O^T += V^T P^T over half j's keys (k-steps u = 2 (j & 1), + 1)
   auto pv = [&](const f32x16_t& s, int j) {
-    const uint8_t* vst = ring + ((j >> 1) & 1) * kSStage + 2 * kSPlane + lane * 8;
+    const uint8_t* vst = ring + kSVBase + ((j >> 1) % 3) * kSPlane + lane * 8;
 #pragma unroll
     for (int ul = 0; ul < 2; ++ul) {
       u32x4_t pf;
@@ -347,8 +354,8 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
     return mx;
   };
 
-  // Prologue: K(tb), V(tb) landed (K(tb + 1) may be in flight); S of half 2 tb and its max.
-  if (tb + 1 < te) wait_vmcnt<4>();
+  // Prologue: tile tb landed (tile tb + 1 may be in flight: 6 DMAs per wave); S of half 2 tb and its max.
+  if (tb + 1 < te) wait_vmcnt<6>();
   else wait_vmcnt<0>();
   __syncthreads();
   f32x16_t sa, sb;
@@ -363,18 +370,18 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
     constexpr bool kMore = decltype(more_tag)::value;
     const int T = j >> 1;
     if ((j & 1) == 0) {
-      // V(T) for this step's PV: issued two half steps ago, K(T + 1) after it
-      if (T + 1 < te) wait_vmcnt<4>();
-      else wait_vmcnt<0>();
-      __syncthreads();
-      if (T + 1 < te) issue_v(T + 1);
+      // tile T landed at step 2T - 1 (or in the prologue): no wait here
       if (wave == 0) fill(T + 2);
     } else {
-      // K(T + 1) for the next half's QK: issued two half steps ago, V(T + 1) after it
-      if (T + 1 < te) wait_vmcnt<2>();
-      else wait_vmcnt<0>();
+      // tile T + 1 (the next half's K, the next step's V), issued two half
+      // steps ago, is the only one in flight; after the barrier every read
+      // of K(T) and V(T - 1) is done, so tile T + 2 takes their places
+      wait_vmcnt<0>();
       __syncthreads();
-      if (T + 2 < te) issue_k(T + 2);
+      if (T + 2 < te) {
+        issue_k(T + 2);
+        issue_v(T + 2);
+      }
     }
     if constexpr (kMore) qk(snext, j + 1);
     exp_half(scur, m_run, sc.c, l_run);
