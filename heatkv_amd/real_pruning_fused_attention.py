@@ -139,9 +139,16 @@ def _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int) -
 def attention_queries_per_item(q_dtype, k_dtype, v_dtype) -> int:
     """Queries per work item of the kernel that :func:`fused_real_pruning_flat_segmented_attention`
     runs for these dtypes at the current dot-mode knobs (the ``queries_per_item``
-    of :func:`segmented_attention_plan`): 256 for the split-row kernel, else 128."""
-    split = _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(), _fused_value_dot_mode_id())
-    return 256 if split else 128
+    of :func:`segmented_attention_plan`), as the library reports it
+    (``hkv_segmented_attention_item_shape``): 128, or 256 for the 8-wave form
+    of the split-row kernel."""
+    qk_mode, value_mode = _fused_qk_dot_mode_id(), _fused_value_dot_mode_id()
+    if not _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode, value_mode):
+        return 128
+    n = int(_lib.load().hkv_segmented_attention_item_shape(
+        _lib.dtype_code(q_dtype), _lib.DTYPE_SPLIT_ROWS, _lib.dtype_code(v_dtype), 1, qk_mode, value_mode, 0, None))
+    _lib.check(min(n, 0))
+    return n
 
 
 def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
@@ -356,7 +363,7 @@ def fused_real_pruning_flat_segmented_attention(
             raise ValueError(f"work_plan must be a contiguous int32 tensor [units, {PLAN_INTS}]")
         if work_plan.device != q.device:
             raise ValueError("work_plan must be on the same device as q")
-        want = 256 if split else 128
+        want = attention_queries_per_item(q.dtype, current_k.dtype, current_v.dtype)
         have = getattr(work_plan, "hkv_queries_per_item", want)
         if have != want:
             raise ValueError(f"work_plan was built for {have}-query items; this call's kernel takes {want} "

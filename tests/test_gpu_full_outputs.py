@@ -46,7 +46,7 @@ def abi_attention(wl, device, *, workspace=True, planned=False, model=False, spl
     """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse
     (``planned``: with the host work plan of its tables; ``model``: fp32 q/k at
     the model's precision, scale 1, see model_precision; ``split_rows``: K
-    passed as split rows, the split-row kernel with 256-query items)."""
+    passed as split rows, the split-row kernel)."""
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
@@ -61,9 +61,12 @@ def abi_attention(wl, device, *, workspace=True, planned=False, model=False, spl
     plan = None
     if planned:
         hst, hen, hct = wl.tables()
+        qpi = 128
+        if split_rows:
+            qpi = _lib.load().hkv_segmented_attention_item_shape(
+                _lib.dtype_code(torch.float32), _lib.DTYPE_SPLIT_ROWS, _lib.dtype_code(cv.dtype), H, 0, 0, 0, None)
         plan = segmented_attention_plan(hst, hen, hct, batch_size=B, current_len=L,
-                                        capacity=wl.schedule.capacity, device=device,
-                                        queries_per_item=256 if split_rows else 128)
+                                        capacity=wl.schedule.capacity, device=device, queries_per_item=qpi)
     stream = torch.cuda.current_stream(device)
     k_args = (slab_k, ck, _lib.dtype_code(ck.dtype))
     if split_rows:

@@ -427,11 +427,11 @@ def test_attention_random_shapes_planned(seed, device, monkeypatch):
 
 @pytest.mark.parametrize("seed", list(range(70, 76)))
 def test_attention_random_shapes_split_rows(seed, device, monkeypatch):
-    """fp32 q/k with bf16 v (the split-row kernel: 256-query items, K written
-    as split rows per call) on random shapes, with the host work plan of
-    256-query items (every other seed without the workspace: cut units run
-    whole) and without a plan, against the oracle; scores of O(10) (q and k
-    of norm ~sqrt(128) / 3.5) so the split's ~16 bits matter."""
+    """fp32 q/k with bf16 v (the split-row kernel, K written as split rows per
+    call) on random shapes, with the host work plan of the kernel's item size
+    (every other seed without the workspace: cut units run whole) and without
+    a plan, against the oracle; scores of O(10) (q and k of norm ~sqrt(128) /
+    3.5) so the split's ~16 bits matter."""
     from heatkv_amd import attention_queries_per_item, segmented_attention_plan
 
     g = torch.Generator().manual_seed(seed)
@@ -444,7 +444,7 @@ def test_attention_random_shapes_split_rows(seed, device, monkeypatch):
         S = 0
     monkeypatch.setenv("HKV_ATTN_SPLIT", "1" if seed % 2 else "0")
     qpi = attention_queries_per_item(torch.float32, torch.float32, torch.bfloat16)
-    assert qpi == 256
+    assert qpi in (128, 256)
     print(f"[attn] split rows random shape seed={seed} B={B} H={H} L={L} cap={cap} S={S}", flush=True)
     q, sk, sv, tables, ck, cv = _random_case(seed, B, H, L, cap, S, dtype=torch.float32, kdtype=torch.float32,
                                              vdtype=torch.bfloat16)
@@ -457,11 +457,12 @@ def test_attention_random_shapes_split_rows(seed, device, monkeypatch):
         out, lse = _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=wp)
         assert_attention_close(to_np(out), to_np(lse), ref_out, ref_lse,
                                 what=f"split rows seed {seed} plan={wp is not None}")
-    # a plan of 128-query items does not fit the split-row kernel
-    if L > 0:
-        plan128 = segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device)
-        with pytest.raises(ValueError, match="128-query items"):
-            _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan128)
+    # a plan of the other item size does not fit the kernel
+    other = 384 - qpi
+    plan_other = segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device,
+                                          queries_per_item=other)
+    with pytest.raises(ValueError, match=f"{other}-query items"):
+        _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan_other)
 
 
 def test_split_rows_bit_exact(device):
