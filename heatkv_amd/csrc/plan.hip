@@ -45,7 +45,7 @@ namespace hkv {
 namespace {
 
 constexpr int kPlanBN = 64;            // keys per tile
-constexpr int kPlanMinPartTiles = 8;   // a part must have this many key tiles
+constexpr int kPlanMinPartTiles = 4;   // a part must have this many key tiles
 constexpr double kUnitOverTiles = 1.5;  // start-up of a workgroup, in key-tile times
 constexpr double kPartOverTiles = 4.0;  // record publish + merge of a part
 constexpr int kNoSearchRounds = 4;     // items per slot above which nothing is cut

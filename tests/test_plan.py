@@ -63,7 +63,7 @@ def _check(plan, st, en, ct, B, L, cap, slots):
     for c, ps in cuts.items():
         assert len(ps) == 2 and ps[0][:2] == ps[1][:2] and {p[2] for p in ps} == {0, 1}
         first = [p for p in ps if p[2] == 0][0]
-        assert first[3] == 0 and first[4] - first[3] >= 8 and tiles[first[0]] - first[4] >= 8
+        assert first[3] == 0 and first[4] - first[3] >= 4 and tiles[first[0]] - first[4] >= 4
     # on each XCD whole units come first, heaviest head first, then the parts
     # longest first (plans without cuts are permuted into XCD groups of equal
     # work instead)
