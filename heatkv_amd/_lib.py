@@ -65,6 +65,7 @@ SIGNATURES = {
         _c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i32]),
     "hkv_segmented_attention_item_shape": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
     "hkv_split_rows": (_c_i32, [_c_p, _c_p, _c_i64, _c_p]),
+    "hkv_concat_kv": (_c_i32, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     "hkv_segmented_attention_slots": (_c_i32, [_c_i32]),
     "hkv_segmented_attention_workspace_bytes": (_c_i64, [_c_i32]),
     "hkv_qkv_produce": (

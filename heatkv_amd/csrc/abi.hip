@@ -140,6 +140,24 @@ int32_t hkv_pack_segments(const void* src_k, const void* src_v, void* dst_k, voi
   return ok();
 }
 
+int32_t hkv_concat_kv(const void* old_k, const void* new_k, const void* old_v, const void* new_v, void* out_k,
+                      void* out_v, int64_t groups, int64_t t_old, int64_t t_new, int64_t k_row_bytes,
+                      int64_t v_row_bytes, void* stream) {
+  if (groups < 0 || t_old < 0 || t_new < 0 || k_row_bytes <= 0 || v_row_bytes <= 0 || k_row_bytes % 2 != 0 ||
+      v_row_bytes % 2 != 0)
+    return fail(HKV_ERR_INVALID_ARG, "groups and row counts must be >= 0 and row sizes positive and even");
+  if (groups == 0 || t_old + t_new == 0) return ok();
+  if (!out_k || !out_v || (t_old > 0 && (!old_k || !old_v)) || (t_new > 0 && (!new_k || !new_v)))
+    return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if ((t_old > t_new ? t_old : t_new) * (k_row_bytes > v_row_bytes ? k_row_bytes : v_row_bytes) >
+      65535LL * 64 * 1024)
+    return fail(HKV_ERR_UNSUPPORTED, "a (batch, head) group of more than 4 GiB");
+  hkv::ConcatArgs a{old_k, new_k, old_v, new_v, out_k, out_v, groups, t_old, t_new, k_row_bytes, v_row_bytes};
+  const hipError_t e = hkv::launch_concat(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HKV_ERR_LAUNCH, "concat launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* slab_v,
                                 const int32_t* seg_starts, const int32_t* seg_ends,
                                 const int32_t* seg_counts, const void* cur_k, const void* cur_v,

@@ -29,6 +29,24 @@ struct PackArgs {
 
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
+// out_k[g] = (old_k[g], new_k[g]) rows, same for V, for `groups` (batch,
+// head) groups of t_old and t_new rows (row sizes in bytes, even).
+struct ConcatArgs {
+  const void* old_k;
+  const void* new_k;
+  const void* old_v;
+  const void* new_v;
+  void* out_k;
+  void* out_v;
+  int64_t groups;
+  int64_t t_old;
+  int64_t t_new;
+  int64_t k_row_bytes;
+  int64_t v_row_bytes;
+};
+
+hipError_t launch_concat(const ConcatArgs& a, hipStream_t stream);
+
 // kSplitRows: fp32 K rows stored as split rows (128 bf16 high parts, then
 // 128 bf16 low parts; 512 bytes a row), the split kernel's K format.
 enum Dtype : int32_t { kF16 = 1, kBF16 = 2, kF32 = 3, kSplitRows = 4 };

@@ -107,7 +107,46 @@ hipError_t launch_v(const PackArgs& a, int uv, dim3 grid, int32_t chunks, hipStr
   return hipGetLastError();
 }
 
+// Dense-prefix growth: out[g] = (old[g] rows, then new[g] rows) for every
+// (batch, head) group g, for K and V in one launch.  blockIdx.y picks the
+// range (old K, new K, old V, new V), blockIdx.z a 64 KiB chunk of it.
+constexpr int64_t kConcatChunk = 64 * 1024;
+
+template <typename U>
+__global__ __launch_bounds__(kThreads) void concat_kernel(ConcatArgs a) {
+  const int64_t g = blockIdx.x;
+  const int part = static_cast<int>(blockIdx.y);
+  const bool is_v = part >= 2;
+  const bool is_new = (part & 1) != 0;
+  const int64_t rb = is_v ? a.v_row_bytes : a.k_row_bytes;
+  const int64_t rows = is_new ? a.t_new : a.t_old;
+  const int64_t bytes = rows * rb;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.z) * kConcatChunk;
+  if (c0 >= bytes) return;
+  const int64_t n = bytes - c0 < kConcatChunk ? bytes - c0 : kConcatChunk;
+  const char* src = static_cast<const char*>(is_v ? (is_new ? a.new_v : a.old_v) : (is_new ? a.new_k : a.old_k));
+  char* dst = static_cast<char*>(is_v ? a.out_v : a.out_k);
+  copy_range<U>(dst + g * (a.t_old + a.t_new) * rb + (is_new ? a.t_old * rb : 0) + c0, src + g * bytes + c0, n);
+}
+
 }  // namespace
+
+hipError_t launch_concat(const ConcatArgs& a, hipStream_t stream) {
+  if (a.groups <= 0 || (a.t_old + a.t_new) <= 0) return hipSuccess;
+  const int64_t most = (a.t_old > a.t_new ? a.t_old : a.t_new) *
+                       (a.k_row_bytes > a.v_row_bytes ? a.k_row_bytes : a.v_row_bytes);
+  const int64_t chunks = (most + kConcatChunk - 1) / kConcatChunk;
+  if (a.groups > 0x7fffffffLL || chunks > 65535) return hipErrorInvalidConfiguration;
+  dim3 grid(static_cast<uint32_t>(a.groups), 4, static_cast<uint32_t>(chunks > 0 ? chunks : 1));
+  // 16-byte units when every range start is 16-byte aligned
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(a.old_k) | reinterpret_cast<uintptr_t>(a.new_k) |
+                         reinterpret_cast<uintptr_t>(a.old_v) | reinterpret_cast<uintptr_t>(a.new_v) |
+                         reinterpret_cast<uintptr_t>(a.out_k) | reinterpret_cast<uintptr_t>(a.out_v);
+  const bool wide = (ptrs % 16) == 0 && a.k_row_bytes % 16 == 0 && a.v_row_bytes % 16 == 0;
+  if (wide) concat_kernel<U16B><<<grid, kThreads, 0, stream>>>(a);
+  else concat_kernel<uint16_t><<<grid, kThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
 
 hipError_t launch_pack(const PackArgs& a, hipStream_t stream) {
   if (a.n_items <= 0 || a.row_limit <= 0 || a.batch <= 0) return hipSuccess;

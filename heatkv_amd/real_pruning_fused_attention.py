@@ -163,6 +163,34 @@ def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
     return out
 
 
+def concat_kv(old_k: torch.Tensor, new_k: torch.Tensor, old_v: torch.Tensor, new_v: torch.Tensor):
+    """``(torch.cat((old_k, new_k), dim=2), torch.cat((old_v, new_v), dim=2))``
+    for ``[B, H, T, D]`` K/V, as one HIP launch (``hkv_concat_kv``): the
+    dense-prefix growth of the segmented cache
+    (enable_real_pruning_fast.py:1972-2038 concatenates K and V separately).
+    No counterpart in the reference module."""
+    for a, b, what in ((old_k, new_k, "K"), (old_v, new_v, "V")):
+        if a.ndim != 4 or b.ndim != 4 or a.shape[:2] != b.shape[:2] or a.shape[3] != b.shape[3]:
+            raise ValueError(f"concat_kv: {what} tensors must be [B, H, T, D] with equal B, H, D")
+        if a.dtype != b.dtype or a.device != b.device:
+            raise ValueError(f"concat_kv: {what} tensors must share dtype and device")
+    if old_k.shape[:3] != old_v.shape[:3] or new_k.shape[:3] != new_v.shape[:3]:
+        raise ValueError("concat_kv: K and V must have the same [B, H, T]")
+    if old_k.device.type != "cuda" or old_v.device != old_k.device:
+        raise RuntimeError("concat_kv requires CUDA tensors")
+    old_k, new_k, old_v, new_v = (t.contiguous() for t in (old_k, new_k, old_v, new_v))
+    B, H, T, Dk = old_k.shape
+    n = new_k.shape[2]
+    Dv = old_v.shape[3]
+    out_k = torch.empty((B, H, T + n, Dk), dtype=old_k.dtype, device=old_k.device)
+    out_v = torch.empty((B, H, T + n, Dv), dtype=old_v.dtype, device=old_v.device)
+    code = _lib.load().hkv_concat_kv(
+        old_k.data_ptr(), new_k.data_ptr(), old_v.data_ptr(), new_v.data_ptr(), out_k.data_ptr(), out_v.data_ptr(),
+        B * H, T, n, Dk * old_k.element_size(), Dv * old_v.element_size(), _lib.stream_handle(old_k.device))
+    _lib.check(code)
+    return out_k, out_v
+
+
 def pack_flat_segments_kv(
     *,
     dst_k: torch.Tensor,

@@ -9,7 +9,8 @@ Control flow, all device work on torch's current stream, no host sync:
 
 * dense prefix (:1972-2038): while no head of this layer is pruned at the
   current target, attention runs over the whole dense cache ``[B, H, T, D]``
-  plus the current scale, and the cache grows by ``torch.cat``; when the next
+  plus the current scale, and the cache grows by concatenation (one HIP
+  launch for K and V, ``concat_kv``); when the next
   target prunes a head, the dense cache is packed into the slab with the
   schedule's activation copy items (:1639-1711 -> :888-908);
 * segmented (:2122-2155): attention over the slab segments of the target's
@@ -35,6 +36,7 @@ import torch
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
     attention_queries_per_item,
+    concat_kv,
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
     segmented_attention_plan,
@@ -258,8 +260,7 @@ class SegmentedLayerCache:
                 if self.cached_k is None or old_len == 0:
                     dense_k, dense_v = k.contiguous(), v.contiguous()
                 else:
-                    dense_k = torch.cat((self.cached_k, k), dim=2)
-                    dense_v = torch.cat((self.cached_v, v), dim=2)
+                    dense_k, dense_v = concat_kv(self.cached_k, k, self.cached_v, v)
                     prof.stat_add("dense_attention_cat_calls")
             self.logical_len = logical
             if has_removed(self.removed(scale_ind + 1)):
@@ -277,7 +278,7 @@ class SegmentedLayerCache:
             with prof.phase("attention"):
                 out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
             with prof.phase("materialize"):
-                dense_candidate = (torch.cat((self.cached_k, k), dim=2), torch.cat((self.cached_v, v), dim=2))
+                dense_candidate = concat_kv(self.cached_k, k, self.cached_v, v)
                 prof.stat_add("dense_attention_cat_calls")
         else:
             with prof.phase("materialize"):
@@ -307,8 +308,7 @@ class SegmentedLayerCache:
                 elif self.cached_k is None or old_len == 0:
                     self.cached_k, self.cached_v = k.contiguous(), v.contiguous()
                 else:
-                    self.cached_k = torch.cat((self.cached_k, k), dim=2)
-                    self.cached_v = torch.cat((self.cached_v, v), dim=2)
+                    self.cached_k, self.cached_v = concat_kv(self.cached_k, k, self.cached_v, v)
             elif self.active:
                 # append the current scale's kept heads (:969-995)
                 prof.stat_add("static_append_current_calls")

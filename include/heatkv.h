@@ -34,6 +34,19 @@ extern "C" {
  * kernel.  No counterpart in the reference. */
 #define HKV_DTYPE_SPLIT_ROWS 4
 
+/*
+ * Dense-prefix growth of the segmented cache in one launch: for each of
+ * `groups` (batch, head) groups, out_k[g] = old_k[g] (t_old rows) followed by
+ * new_k[g] (t_new rows), and the same for V; rows of k_row_bytes /
+ * v_row_bytes bytes, every tensor contiguous ([groups, rows, ...]).  What
+ * torch.cat((old_k, new_k), dim=2) and the same for V give, as one kernel.
+ * Replaces the two concatenations of the reference's dense prefix
+ * (enable_real_pruning_fast.py:1972-2038).
+ */
+int32_t hkv_concat_kv(const void* old_k, const void* new_k, const void* old_v, const void* new_v, void* out_k,
+                      void* out_v, int64_t groups, int64_t t_old, int64_t t_new, int64_t k_row_bytes,
+                      int64_t v_row_bytes, void* stream);
+
 /* Library version, (major << 16) | (minor << 8) | patch. Loader check. */
 int32_t hkv_version(void);
 

@@ -495,3 +495,22 @@ def test_split_rows_bit_exact(device):
     lo = bf16_rne((xn - hi_f).astype(np.float32))
     assert np.array_equal(got[:, :128], hi)
     assert np.array_equal(got[:, 128:], lo)
+
+
+@pytest.mark.parametrize("kdt,vdt,T,n", [(torch.bfloat16, torch.bfloat16, 21, 36), (torch.float32, torch.bfloat16, 0, 4),
+                                         (torch.float16, torch.float16, 57, 0), (torch.float32, torch.float32, 600, 700)])
+def test_concat_kv_bit_exact(kdt, vdt, T, n, device):
+    """concat_kv (one launch for K and V) equals torch.cat of each, bit for bit,
+    including empty old or new parts and groups larger than one 64 KiB chunk."""
+    from heatkv_amd.real_pruning_fused_attention import concat_kv
+
+    g = torch.Generator().manual_seed(T + n)
+    B, H, D = 2, 3, 128
+    ok, nk = (torch.randn((B, H, t, D), generator=g).to(kdt).to(device) for t in (T, n))
+    ov, nv = (torch.randn((B, H, t, D), generator=g).to(vdt).to(device) for t in (T, n))
+    out_k, out_v = concat_kv(ok, nk, ov, nv)
+    torch.cuda.synchronize(device)
+    for got, want in ((out_k, torch.cat((ok, nk), dim=2)), (out_v, torch.cat((ov, nv), dim=2))):
+        assert got.shape == want.shape and got.dtype == want.dtype
+        assert torch.equal(got.view(torch.int16 if got.element_size() == 2 else torch.int32),
+                           want.view(torch.int16 if want.element_size() == 2 else torch.int32))

@@ -1,7 +1,8 @@
 """Host control flow of SegmentedLayerCache on the CPU (no GPU, no HIP).
 
-The two HIP operators are replaced, for this test only, by CPU restatements
-from oracle/ (attention: oracle/segmented_attention.py; pack: oracle/pack.py)
+The HIP operators are replaced, for this test only, by CPU restatements
+from oracle/ (attention: oracle/segmented_attention.py; pack: oracle/pack.py;
+the dense-prefix concatenation: torch.cat, what it computes)
 so the dense prefix -> activation -> segmented -> append -> reset flow of
 enable_real_pruning_fast.py:1951-2254 can be checked here: every step's
 output must equal attention over the keys a static keep policy retains, the
@@ -39,10 +40,15 @@ def _cpu_pack(*, dst_k, dst_v, src_k, src_v, dst_starts, src_starts, lengths, ma
     return dst_k, dst_v
 
 
+def _cpu_concat(old_k, new_k, old_v, new_v):
+    return torch.cat((old_k, new_k), dim=2), torch.cat((old_v, new_v), dim=2)
+
+
 @pytest.fixture
 def cpu_ops(monkeypatch):
     monkeypatch.setattr(sc, "fused_real_pruning_flat_segmented_attention", _cpu_attention)
     monkeypatch.setattr(sc, "pack_flat_segments_kv", _cpu_pack)
+    monkeypatch.setattr(sc, "concat_kv", _cpu_concat)
 
 
 def _expected(inputs, keep, t, scale):
