@@ -55,6 +55,12 @@ SIGNATURES = {
          _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
          _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p],
     ),
+    "hkv_segmented_attention_append": (
+        _c_i32,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
+         _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
+         _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_p],
+    ),
     "hkv_segmented_attention_noalloc": (
         _c_i32,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,

@@ -168,6 +168,25 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 int32_t qk_dot_mode, int32_t value_dot_mode,
                                 const int32_t* work_plan, int32_t plan_units,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  // without append offsets the slab is only read
+  return hkv_segmented_attention_append(q, const_cast<void*>(slab_k), const_cast<void*>(slab_v), seg_starts,
+                                        seg_ends, seg_counts, cur_k, cur_v, out, lse, batch, heads, cur_len,
+                                        slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype,
+                                        softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, work_plan, plan_units,
+                                        workspace, workspace_bytes, nullptr, stream);
+}
+
+int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v,
+                                       const int32_t* seg_starts, const int32_t* seg_ends,
+                                       const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                       void* out, float* lse, int32_t batch, int32_t heads,
+                                       int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                       int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                       int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                       int32_t qk_dot_mode, int32_t value_dot_mode,
+                                       const int32_t* work_plan, int32_t plan_units,
+                                       void* workspace, int64_t workspace_bytes, const int32_t* append_offsets,
+                                       void* stream) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (qk_dot_mode < 0 || qk_dot_mode > 2)
     return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
@@ -229,6 +248,14 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   if (slab_capacity * row_bytes >= 0x7fffffffLL || static_cast<int64_t>(cur_len) * row_bytes >= 0x7fffffffLL)
     return fail(HKV_ERR_UNSUPPORTED, "slab rows per batch row and current_len must stay below %lld",
                 static_cast<long long>(0x7fffffffLL / row_bytes));
+  if (append_offsets != nullptr) {
+    // the copy moves whole rows 16 bytes per access
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(slab_k) | reinterpret_cast<uintptr_t>(slab_v) |
+                           reinterpret_cast<uintptr_t>(cur_k) | reinterpret_cast<uintptr_t>(cur_v);
+    if (slab_capacity < cur_len || (bits & 15) != 0)
+      return fail(HKV_ERR_INVALID_ARG,
+                  "the append needs slab_capacity >= current_len and 16-byte aligned slab and current tensors");
+  }
   hkv::AttnArgs a{};
   a.q = q;
   a.slab_k = slab_k;
@@ -256,6 +283,7 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
   a.workspace_bytes = workspace != nullptr ? workspace_bytes : 0;
   a.plan = work_plan;
   a.plan_units = work_plan != nullptr ? plan_units : 0;
+  a.append_offsets = append_offsets;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));

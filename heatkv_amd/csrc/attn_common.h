@@ -859,6 +859,53 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The current rows' append (AttnArgs::append_offsets).  A copy block moves
+// kAppendRows rows of K and of V of one (b, h), 16 bytes per lane per access
+// (one access per lane and tensor for 16-bit rows); heads with off < 0 or
+// off + L > capacity are skipped.  The rows written lie outside every segment
+// the launch reads (the caller's contract), so copy blocks and attention
+// workgroups of one launch need no ordering.
+constexpr int kAppendRows = 16;
+
+__host__ __device__ inline int64_t append_blocks(int32_t batch, int32_t heads, int32_t L) {
+  return static_cast<int64_t>(batch) * heads * ((L + kAppendRows - 1) / kAppendRows);
+}
+
+template <int kThreads>
+__device__ __forceinline__ void append_block(const AttnArgs& a, uint32_t blk, int32_t k_row, int32_t v_row) {
+  const int32_t L = a.cur_len;
+  const uint32_t H = static_cast<uint32_t>(a.heads);
+  const int64_t cap = a.slab_capacity;
+  // 32-bit index arithmetic: blocks and (b, h) pairs fit a launch grid
+  const uint32_t chunks = static_cast<uint32_t>((L + kAppendRows - 1) / kAppendRows);
+  const uint32_t bh = blk / chunks;
+  if (bh >= static_cast<uint32_t>(a.batch) * H) return;
+  const int32_t h = static_cast<int32_t>(bh % H);
+  const int64_t b = bh / H;
+  const int32_t off = a.append_offsets[h];
+  if (off < 0 || off > cap - L) return;
+  const int32_t r0 = static_cast<int32_t>(blk - bh * chunks) * kAppendRows;
+  const int32_t rows = L - r0 < kAppendRows ? L - r0 : kAppendRows;
+  const int64_t dst_row = b * cap + off + r0;
+  const int64_t src_row = static_cast<int64_t>(bh) * L + r0;
+  const uint4* sk = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.cur_k) + src_row * k_row);
+  const uint4* sv = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.cur_v) + src_row * v_row);
+  uint4* dk = reinterpret_cast<uint4*>(static_cast<uint8_t*>(const_cast<void*>(a.slab_k)) + dst_row * k_row);
+  uint4* dv = reinterpret_cast<uint4*>(static_cast<uint8_t*>(const_cast<void*>(a.slab_v)) + dst_row * v_row);
+  const int32_t nk = rows * (k_row / 16);
+  const int32_t nv = rows * (v_row / 16);
+  // one access of each tensor in flight per lane: more (a deeper batch of
+  // loads) makes the 16-bit kernel's register allocation spill
+  const int32_t n = nk > nv ? nk : nv;
+  for (int32_t u = static_cast<int32_t>(threadIdx.x); u < n; u += kThreads) {
+    uint4 xk, xv;
+    if (u < nk) xk = sk[u];
+    if (u < nv) xv = sv[u];
+    if (u < nk) dk[u] = xk;
+    if (u < nv) dv[u] = xv;
+  }
+}
+
 }  // namespace attn
 
 hipError_t launch_attention_direct(const AttnArgs& a, const attn::Scalars& s, hipStream_t stream);

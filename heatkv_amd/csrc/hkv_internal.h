@@ -84,6 +84,11 @@ struct AttnArgs {
   const int32_t* plan;      // work plan (kPlanInts ints per unit), or null: planned in the kernel
   int32_t plan_units;
   int32_t ws_cuts;          // cut items the workspace holds (set by the launch)
+  // Append of the current rows for the next scale, or null: current rows
+  // [0, L) of (b, h) go to slab rows [off, off + L) of batch row b, off =
+  // append_offsets[h] (-1: head h is not copied).
+  const int32_t* append_offsets;
+  int32_t append_first;     // first copy workgroup of a fused launch (set by the launch)
 };
 
 // Work plan units (build_attention_plan): head, index in the head

@@ -101,6 +101,11 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   __shared__ int32_t merge_turn;
   static_assert(NS * kStageBytes >= 2 * kMaxHeads * 4, "head tables alias the ring");
 
+  if (a.append_offsets != nullptr && static_cast<int32_t>(blockIdx.x) >= a.append_first) {
+    // a copy block of the fused append, after the attention workgroups
+    append_block<256>(a, blockIdx.x - static_cast<uint32_t>(a.append_first), kD * 2, kD * 2);
+    return;
+  }
   const int64_t cap = a.slab_capacity;
   const int H = a.heads;
   const int L = a.cur_len;
@@ -419,13 +424,13 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
     const int64_t by_records = (a.workspace_bytes - kCounterBytes) / (2LL * kPartialFloats * 4);
     b.ws_cuts = static_cast<int32_t>(by_records < kCounterBytes / 4 ? by_records : kCounterBytes / 4);
   }
-  if (a.plan != nullptr) {
-    if (a.plan_units <= 0) return hipSuccess;
-    seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(a.plan_units)), 256, 0, st>>>(b, s, n_qt, split);
-    return hipGetLastError();
-  }
-  const int64_t blocks = split_units(split);
-  seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks)), 256, 0, st>>>(b, s, n_qt, split);
+  // the fused append's copy blocks follow the attention workgroups
+  const int64_t copies = a.append_offsets != nullptr ? append_blocks(a.batch, a.heads, a.cur_len) : 0;
+  const int64_t blocks = a.plan != nullptr ? (a.plan_units > 0 ? a.plan_units : 0) : split_units(split);
+  if (blocks + copies <= 0) return hipSuccess;
+  if (blocks + copies > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  b.append_first = static_cast<int32_t>(blocks);
+  seg_attn_pipe_kernel<DT, DT, VDT><<<dim3(static_cast<uint32_t>(blocks + copies)), 256, 0, st>>>(b, s, n_qt, split);
   return hipGetLastError();
 }
 

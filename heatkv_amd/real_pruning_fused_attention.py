@@ -151,6 +151,13 @@ def attention_queries_per_item(q_dtype, k_dtype, v_dtype) -> int:
     return n
 
 
+def attention_fuses_append(q_dtype, k_dtype, v_dtype) -> bool:
+    """Whether :func:`fused_real_pruning_flat_segmented_attention` takes
+    ``append_offsets`` for these dtypes at the current dot-mode knobs (every
+    path but the split-row one, whose slab K is a split copy)."""
+    return not _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(), _fused_value_dot_mode_id())
+
+
 def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
     """fp32 ``[..., 128]`` rows as split rows ``[..., 256]`` bf16 (128 high
     parts, then 128 low parts), by the HIP kernel ``hkv_split_rows``."""
@@ -284,6 +291,7 @@ def fused_real_pruning_flat_segmented_attention(
     return_lse: bool = False,
     out_dtype: Optional[torch.dtype] = None,
     work_plan: Optional[torch.Tensor] = None,
+    append_offsets: Optional[torch.Tensor] = None,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
 
@@ -294,7 +302,13 @@ def fused_real_pruning_flat_segmented_attention(
     would give), and ``lse [B, H, L]`` fp32 when ``return_lse``.  ``work_plan``
     (an extension): the plan :func:`segmented_attention_plan` built for these
     same tables, batch size and current length, on q's device; the kernel then
-    skips ordering its work itself.  Mirrors fused_real_pruning_flat_segmented_attention
+    skips ordering its work itself.  ``append_offsets`` (an extension): int32
+    ``[H]`` on q's device; the same launch then also writes current rows
+    ``[0, L)`` of (b, h) to slab rows ``[off, off + L)`` of batch row b, off =
+    ``append_offsets[h]`` (-1: not written) -- the append that follows the
+    attention in the reference's cache update, for rows outside every segment
+    this call reads (:func:`attention_fuses_append` says which inputs take it).
+    Mirrors fused_real_pruning_flat_segmented_attention
     (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
     ``hkv_segmented_attention``.
     """
@@ -369,6 +383,8 @@ def fused_real_pruning_flat_segmented_attention(
     value_mode = _fused_value_dot_mode_id()
 
     _lib.require_device(q.device)
+    if append_offsets is not None and not (persisted_k.is_contiguous() and persisted_v.is_contiguous()):
+        raise ValueError("append_offsets: the slab must be contiguous (the append writes it in place)")
     q = q.contiguous()
     persisted_k = persisted_k.contiguous()
     persisted_v = persisted_v.contiguous()
@@ -396,6 +412,16 @@ def fused_real_pruning_flat_segmented_attention(
         if have != want:
             raise ValueError(f"work_plan was built for {have}-query items; this call's kernel takes {want} "
                              "(segmented_attention_plan(..., queries_per_item=attention_queries_per_item(...)))")
+    if append_offsets is not None:
+        if split:
+            raise ValueError("append_offsets: the split-row K path writes a split copy of the slab; "
+                             "append after the call (attention_fuses_append)")
+        if (append_offsets.dtype != torch.int32 or tuple(append_offsets.shape) != (num_heads,)
+                or append_offsets.device != q.device):
+            raise ValueError("append_offsets must be an int32 tensor [H] on q's device")
+        if persisted_k.dtype != current_k.dtype or persisted_v.dtype != current_v.dtype:
+            raise ValueError("append_offsets: the slab and the current rows must share their dtypes")
+        append_offsets = append_offsets.contiguous()
     stream = torch.cuda.current_stream(q.device)
     ws = _lib.attention_workspace(q.device, stream)
     k_code = _lib.dtype_code(current_k.dtype)
@@ -404,7 +430,7 @@ def fused_real_pruning_flat_segmented_attention(
         persisted_k = _split_rows(persisted_k, stream)
         current_k = _split_rows(current_k, stream)
         k_code = _lib.DTYPE_SPLIT_ROWS
-    code = _lib.load().hkv_segmented_attention(
+    args = (
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
         segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
         current_k.data_ptr(), current_v.data_ptr(), output.data_ptr(),
@@ -416,8 +442,11 @@ def fused_real_pruning_flat_segmented_attention(
         work_plan.data_ptr() if work_plan is not None else None,
         int(work_plan.shape[0]) if work_plan is not None else 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
-        stream.cuda_stream,
     )
+    if append_offsets is None:
+        code = _lib.load().hkv_segmented_attention(*args, stream.cuda_stream)
+    else:
+        code = _lib.load().hkv_segmented_attention_append(*args, append_offsets.data_ptr(), stream.cuda_stream)
     _lib.check(code)
     if return_lse:
         return output, lse

@@ -35,6 +35,7 @@ import torch
 
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
+    attention_fuses_append,
     attention_queries_per_item,
     concat_kv,
     fused_real_pruning_flat_segmented_attention,
@@ -66,6 +67,15 @@ def work_plans_enabled(device) -> bool:
     the capture, so that replays compute exactly what eager calls compute,
     and none if there was no such call."""
     return _env_flag("HKV_ATTN_PLAN", True) and torch.device(device).type == "cuda"
+
+
+def fused_append_enabled() -> bool:
+    """HKV_FUSED_APPEND (default on): the attention launch of a step also
+    writes the current rows that the append for the next scale places outside
+    every segment it reads (``append_offsets``); the copy after it moves only
+    the rest.  Under HIP-graph capture only a split made by an eager call is
+    used."""
+    return _env_flag("HKV_FUSED_APPEND", True)
 
 
 def _capturing() -> bool:
@@ -234,6 +244,15 @@ class SegmentedLayerCache:
             return None
         return self.cached_k, self.cached_v, offsets
 
+    def _fused_append_offsets(self, scale_ind: int, q, k, v) -> Optional[torch.Tensor]:
+        """``append_offsets`` of this step's attention launch, or None."""
+        if not fused_append_enabled() or not attention_fuses_append(q.dtype, k.dtype, v.dtype):
+            return None
+        if self.cached_k.dtype != k.dtype or self.cached_v.dtype != v.dtype:
+            return None
+        hit = self.schedule.fused_append(int(scale_ind), k.device, build=not _capturing())
+        return None if hit is None else hit[0]
+
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale_ind: int,
              softmax_scale: float, softmax_mode: Optional[str] = None, appended: bool = False,
              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
@@ -271,6 +290,7 @@ class SegmentedLayerCache:
             return out
 
         dense_candidate = None
+        fused = False
         if old_len == 0:
             with prof.phase("attention"):
                 out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
@@ -290,12 +310,14 @@ class SegmentedLayerCache:
                                                        queries_per_item=attention_queries_per_item(
                                                            q.dtype, k.dtype, v.dtype))
                         if work_plans_enabled(q.device) else None)
+                offsets = None if final or appended else self._fused_append_offsets(scale_ind, q, k, v)
+                fused = offsets is not None
             with prof.phase("attention"):
                 out = fused_real_pruning_flat_segmented_attention(
                     q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
                     segment_starts=starts, segment_ends=ends, segment_counts=counts,
                     current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
-                    out_dtype=out_dtype, work_plan=plan)
+                    out_dtype=out_dtype, work_plan=plan, append_offsets=offsets)
 
         with prof.phase("compact"):
             if final:
@@ -312,7 +334,8 @@ class SegmentedLayerCache:
             elif self.active:
                 # append the current scale's kept heads (:969-995)
                 prof.stat_add("static_append_current_calls")
-                if appended:
+                if appended or fused:
+                    # the producer or the attention launch wrote the offered heads
                     _, plan = self.schedule.fused_append(int(scale_ind), k.device)
                     tag = ("append_rest", int(scale_ind))
                 else:

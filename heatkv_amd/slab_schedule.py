@@ -152,7 +152,8 @@ class SlabSchedule:
             self._device_cache[key] = hit
         return hit
 
-    def fused_append(self, scale: int, device) -> Tuple[Optional[torch.Tensor], CopyPlan]:
+    def fused_append(self, scale: int, device, *,
+                     build: bool = True) -> Optional[Tuple[Optional[torch.Tensor], CopyPlan]]:
         """Split of the append of ``scale`` (plan ``(scale, scale + 1)``) for a
         producer that writes K/V rows before this scale's attention runs.
 
@@ -161,10 +162,11 @@ class SlabSchedule:
         outside all segments live at ``scale`` (the rows the attention reads),
         -1 for the others (None when no head qualifies); ``residual`` is the
         plan of the heads left to the copy after attention.  Cached per
-        (device, scale)."""
+        (device, scale); with ``build=False`` only a split already made is
+        returned (None otherwise)."""
         key = ("fused_append", str(device), int(scale))
         hit = self._device_cache.get(key)
-        if hit is not None:
+        if hit is not None or not build:
             return hit
         plan = self.append_plans.get((int(scale), int(scale) + 1))
         if plan is None or len(plan) == 0:

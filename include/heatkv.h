@@ -159,6 +159,38 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * hkv_segmented_attention followed by the append of the current rows for
+ * the next scale, in one launch with the 16-bit kernel (its copy workgroups
+ * follow the attention workgroups) and in a second launch on `stream`
+ * otherwise.  Replaces the attention call plus the static append of the
+ * kept heads' current rows that follows it (enable_real_pruning_fast.py:
+ * 1791-1807 -> 969-995) when every destination row lies outside the segments
+ * this call reads.
+ *   append_offsets : int32 [heads] on the device: current rows [0, cur_len)
+ *                    of (b, h) are written to slab rows [off, off + cur_len)
+ *                    of batch row b, off = append_offsets[h]; heads with
+ *                    off < 0 or off + cur_len > slab_capacity are not
+ *                    copied.  The rows written must not lie in any segment
+ *                    of seg_starts / seg_ends (then the results are those of
+ *                    the two calls in order; otherwise undefined).  NULL:
+ *                    the call is hkv_segmented_attention.
+ * The slab and current tensors must be 16-byte aligned and slab_capacity >=
+ * cur_len.  Other arguments and results as hkv_segmented_attention.
+ */
+int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v,
+                                       const int32_t* seg_starts, const int32_t* seg_ends,
+                                       const int32_t* seg_counts, const void* cur_k,
+                                       const void* cur_v, void* out, float* lse,
+                                       int32_t batch, int32_t heads, int32_t cur_len,
+                                       int64_t slab_capacity, int32_t max_segments, int32_t head_dim,
+                                       int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                       int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                       int32_t qk_dot_mode, int32_t value_dot_mode,
+                                       const int32_t* work_plan, int32_t plan_units,
+                                       void* workspace, int64_t workspace_bytes,
+                                       const int32_t* append_offsets, void* stream);
+
+/*
  * Work plan of hkv_segmented_attention for host copies of its offset tables
  * (int32 seg_starts / seg_ends [heads, max_segments], seg_counts [heads]),
  * batch and cur_len, for items of `queries_per_item` queries (128, or 256

@@ -514,3 +514,75 @@ def test_concat_kv_bit_exact(kdt, vdt, T, n, device):
         assert got.shape == want.shape and got.dtype == want.dtype
         assert torch.equal(got.view(torch.int16 if got.element_size() == 2 else torch.int32),
                            want.view(torch.int16 if want.element_size() == 2 else torch.int32))
+
+
+@pytest.mark.parametrize("seed,qkdt,vdt,planned,split", [
+    (80, torch.bfloat16, torch.bfloat16, True, "1"), (81, torch.bfloat16, torch.bfloat16, False, "1"),
+    (82, torch.float16, torch.float16, True, "0"), (83, torch.bfloat16, torch.float16, False, "0"),
+    (84, torch.float32, torch.float32, True, "1"), (85, torch.float32, torch.bfloat16, False, "1"),
+    (86, torch.bfloat16, torch.bfloat16, True, "0")])
+def test_attention_fused_append(seed, qkdt, vdt, planned, split, device, monkeypatch):
+    """append_offsets (hkv_segmented_attention_append): the output and LSE
+    equal the plain call's bit for bit, and the slab afterwards equals the
+    slab with each appended head's current rows written at its offset (heads
+    at -1 and one whose rows would pass the capacity untouched), on random
+    shapes whose segments stay below the appended rows; the 16-bit kernel
+    runs the copy in its own launch, the register-staged kernel (fp32 K or V)
+    after it."""
+    from heatkv_amd import segmented_attention_plan
+
+    monkeypatch.setenv("HKV_ATTN_SPLIT", split)
+    monkeypatch.setenv("HKV_ATTN_SPLIT_ROWS", "0")  # fp32 q/k with bf16 v on the staged kernel
+    g = torch.Generator().manual_seed(seed)
+
+    def pick(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    B, H, L, cap0, S = pick(1, 3), pick(2, 24), pick(1, 700), pick(0, 3000), pick(0, 20)
+    if cap0 == 0:
+        S = 0
+    cap = cap0 + H * L
+    print(f"[attn] fused append seed={seed} B={B} H={H} L={L} cap={cap} S={S} {qkdt} {vdt} "
+          f"planned={planned} split={split}", flush=True)
+    q, sk0, sv0, tables, ck, cv = _random_case(seed, B, H, L, cap0, S, dtype=qkdt, kdtype=qkdt, vdtype=vdt)
+    # rows [cap0, cap) hold H slots of L rows above every segment
+    sk = torch.cat((sk0, torch.randn((B, H * L, 128), generator=g).to(qkdt)), dim=1)
+    sv = torch.cat((sv0, torch.randn((B, H * L, 128), generator=g).to(vdt)), dim=1)
+    slots = torch.randperm(H, generator=g).tolist()
+    offsets = [cap0 + slots[h] * L if bool(torch.rand((1,), generator=g) < 0.75) else -1 for h in range(H)]
+    offsets[-1] = cap - L + 1  # past the capacity: not written
+    want_k, want_v = sk.clone(), sv.clone()
+    for h, off in enumerate(offsets):
+        if 0 <= off <= cap - L:
+            want_k[:, off:off + L] = ck[:, h]
+            want_v[:, off:off + L] = cv[:, h]
+    plan = (segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device)
+            if planned else None)
+    scale = 1.0 / math.sqrt(128)
+    out_a, lse_a = _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan)
+    slab_k, slab_v = sk.to(device), sv.to(device)
+    out_b, lse_b = _run(q, slab_k, slab_v, tables, ck, cv, scale, device, work_plan=plan,
+                        append_offsets=torch.tensor(offsets, dtype=torch.int32, device=device))
+    assert np.array_equal(bits(out_b), bits(out_a))
+    assert np.array_equal(bits(lse_b), bits(lse_a))
+    assert np.array_equal(bits(slab_k), bits(want_k))
+    assert np.array_equal(bits(slab_v), bits(want_v))
+
+
+def test_attention_fused_append_rejects(device, monkeypatch):
+    """append_offsets is refused where the call would not write the caller's
+    slab: the split-row K path (a split copy of the slab) and a slab that is
+    not contiguous; and for a wrongly shaped offsets tensor."""
+    monkeypatch.setenv("HKV_ATTN_SPLIT_ROWS", "1")
+    B, H, L, cap = 1, 2, 8, 64
+    q, sk, sv, tables, ck, cv = _random_case(90, B, H, L, cap, 2, dtype=torch.float32, kdtype=torch.float32,
+                                             vdtype=torch.bfloat16)
+    offs = torch.tensor([0, 8], dtype=torch.int32, device=device)
+    with pytest.raises(ValueError, match="split"):
+        _run(q, sk, sv, tables, ck, cv, 0.1, device, append_offsets=offs)
+    q, sk, sv, tables, ck, cv = _random_case(91, B, H, L, cap, 2)
+    wide_k = torch.zeros((B, cap, 256), dtype=sk.dtype, device=device)
+    with pytest.raises(ValueError, match="contiguous"):
+        _run(q, wide_k[:, :, :128], sv, tables, ck, cv, 0.1, device, append_offsets=offs)
+    with pytest.raises(ValueError, match=r"\[H\]"):
+        _run(q, sk, sv, tables, ck, cv, 0.1, device, append_offsets=offs[:1])

@@ -54,13 +54,16 @@ def _reference(inputs, ctrl, layer, t, scale, heads, batches):
     return out
 
 
-@pytest.mark.parametrize("layer", [0, 29])
-def test_generation_under_reference_policy(device, layer):
+@pytest.mark.parametrize("layer,fused", [(0, "1"), (29, "1"), (0, "0")])
+def test_generation_under_reference_policy(device, monkeypatch, layer, fused):
+    # fused "1": appends whose rows lie outside the step's segments ride on its
+    # attention launch (layer 0 has them at scales 8-11, next to copied heads)
+    monkeypatch.setenv("HKV_FUSED_APPEND", fused)
     orders = json.load(open(os.path.join(HERE, "golden", "orders_2b.json")))
     ctrl = P.controller_for_budget(0.1, orders, num_layers=L_MODEL, num_heads=H, protected_prefix_scales=START)
     sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
     dropped = sum(1 for g in sched.segments if g.end_target < len(SIDES_1M))
-    print(f"[policy gen] layer {layer} capacity {sched.capacity} segments {len(sched.segments)} "
+    print(f"[policy gen] layer {layer} fused {fused} capacity {sched.capacity} segments {len(sched.segments)} "
           f"dropped part-way {dropped}", flush=True)
     cache = sc.SegmentedLayerCache(sched, lambda t: ctrl.removed_heads_by_source_for(layer, t), num_heads=H)
     B = 2

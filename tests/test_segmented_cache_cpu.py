@@ -24,7 +24,15 @@ from oracle import segmented_attention as oattn
 
 
 def _cpu_attention(*, q, persisted_k, persisted_v, segment_starts, segment_ends, segment_counts,
-                   current_k, current_v, softmax_scale, softmax_mode="exp", **_):
+                   current_k, current_v, softmax_scale, softmax_mode="exp", append_offsets=None, **_):
+    if append_offsets is not None:
+        # the fused append, written before the attention reads the slab: a
+        # row that a segment of this call covered would change the result
+        L = current_k.shape[2]
+        for h, off in enumerate(append_offsets.tolist()):
+            if 0 <= off <= persisted_k.shape[1] - L:
+                persisted_k[:, off:off + L] = current_k[:, h]
+                persisted_v[:, off:off + L] = current_v[:, h]
     f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
     out, _ = oattn.flat_segmented_attention(
         f(q), f(persisted_k), f(persisted_v), segment_starts.numpy(), segment_ends.numpy(),
@@ -114,21 +122,35 @@ def test_unpruned_policy_stays_dense(cpu_ops):
         assert cache.cached_k.shape[2] == sum(s * s for s in sides[:t + 1])
 
 
-def test_generation_flow_under_reference_policy(cpu_ops):
+@pytest.mark.parametrize("layer", [7, 0])
+@pytest.mark.parametrize("fused_append", ["1", "0"])
+def test_generation_flow_under_reference_policy(cpu_ops, monkeypatch, fused_append, layer):
     """The 13-scale generation of one layer under the reference's HeatKV
     policy (orders/2b.json, budget 0.1, first source scale 3; pinned by
     tests/test_policy.py): heads are dropped part-way, freed slab rows are
     reused by later appends, and every step still equals attention over the
-    keys the policy keeps (head_dim 16 to keep the CPU run short)."""
+    keys the policy keeps (head_dim 16 to keep the CPU run short).  With
+    HKV_FUSED_APPEND on, the appends ride on the attention calls (the host
+    stand-in writes them before it reads the slab)."""
     import json
     import os
+
+    monkeypatch.setenv("HKV_FUSED_APPEND", fused_append)
+    fused_calls = []
+
+    def counting_attention(**kw):
+        if kw.get("append_offsets") is not None:
+            fused_calls.append(int((kw["append_offsets"] >= 0).sum()))
+        return _cpu_attention(**kw)
+
+    monkeypatch.setattr(sc, "fused_real_pruning_flat_segmented_attention", counting_attention)
 
     from heatkv_amd import policy as P
     from heatkv_amd.slab_schedule import SIDES_1M, build_static_slot_schedule
 
     here = os.path.dirname(os.path.abspath(__file__))
     orders = json.load(open(os.path.join(here, "golden", "orders_2b.json")))
-    H, layer = 16, 7
+    H = 16
     ctrl = P.controller_for_budget(0.1, orders, num_layers=32, num_heads=H, protected_prefix_scales=3)
     sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
     assert any(g.end_target < len(SIDES_1M) for g in sched.segments)  # progressive removal
@@ -152,6 +174,12 @@ def test_generation_flow_under_reference_policy(cpu_ops):
                 got = cache.cached_k[:, seg.offset:seg.offset + seg.length]
                 assert torch.equal(got, inputs[seg.source_scale][1][:, seg.head]), (t, seg)
     assert cache.cached_k is None
+    if fused_append == "1":
+        # layer 7 fuses one head's append at scale 9; layer 0 fuses most heads
+        # at scales 8-11 and copies the rest after the attention
+        assert sum(fused_calls) > 0 and (layer != 0 or len(fused_calls) == 4), fused_calls
+    else:
+        assert not fused_calls
 
 
 def test_fused_append_split_under_reference_policy(cpu_ops):
