@@ -121,8 +121,11 @@ def attention_call(wl, device):
 
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
+    from heatkv_amd import attention_queries_per_item
+
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
-    plan = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len)
+    plan = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len,
+                                         queries_per_item=attention_queries_per_item(q.dtype, ck.dtype, cv.dtype))
             if work_plans_enabled(device) else None)
     return dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
                 segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale,
