@@ -27,7 +27,10 @@ Precision: the reference runs its dense-prefix scales through the model's own
 flash attention with q and k cast to bf16 (basic.py:296-302) and its
 segmented scales with fp32 q and k (a TF32 product); here every scale attends
 with the fp32 q and k of the producer (split-bf16 products, about 16
-significand bits).  With ``REAL_PRUNING_FUSED_QK_DOT_MODE=tf32`` (the
+significand bits); the producer writes that K as split rows (bf16 high and
+low parts, the split-row kernel's K format), so the cache keeps K in that
+form and no attention call splits it again.  With
+``REAL_PRUNING_FUSED_QK_DOT_MODE=tf32`` (the
 reference's knob for TF32 q/k products) a cosine-attention layer's producer
 writes q and k as fp16 instead: the same 11-bit significand as TF32, exact
 range for cosine attention (|k| = 1, |q| <= exp(max_scale_mul)), half the K
@@ -41,7 +44,7 @@ import torch
 import torch.nn.functional as F
 
 from .produce import qkv_produce, rope_start, rope_table_for, scale_mul_of
-from .real_pruning_fused_attention import _fused_qk_dot_mode_id
+from .real_pruning_fused_attention import _fused_qk_dot_mode_id, split_rows_k_format
 
 _QK_DOT_TF32 = 1
 
@@ -106,17 +109,20 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
     qk_dtype = torch.float32 if (cos_attn or table is not None) else torch.bfloat16
     if cos_attn and _fused_qk_dot_mode_id() == _QK_DOT_TF32:
         qk_dtype = torch.float16
+    # fp32 K that the attention reads as split rows is written in that form
+    # by the producer (and kept so in the cache), so no call splits it again
+    k_split = split_rows_k_format(qk_dtype, qk_dtype, torch.bfloat16)
     cache = self.heatkv_cache
     append = cache.producer_append(int(scale_ind), qk_dtype, qkv.device)
     q, k, v = qkv_produce(
         qkv.view(batch_size, seq_len, 3 * self.num_heads * self.head_dim), self.num_heads,
         scale_mul=_scale_mul(self) if cos_attn else None, rope_table=table, rope_start_row=start,
-        normalize=cos_attn, qk_dtype=qk_dtype, append=append)
+        normalize=cos_attn, qk_dtype=qk_dtype, append=append, k_split_rows=k_split)
     del qkv
     # under autocast the projection takes the attention output in the autocast
     # dtype: the kernel writes it rounded once, as autocast's cast would
     output = cache.step(q, k, v, int(scale_ind), float(self.scale), appended=append is not None,
-                        out_dtype=_autocast_dtype(x))
+                        out_dtype=_autocast_dtype(x), k_split_rows=k_split)
     return self.proj_drop(self.proj(output))
 
 

@@ -300,8 +300,11 @@ int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bi
   if (head_dim != 128) return fail(HKV_ERR_UNSUPPORTED, "qkv producer supports head_dim=128 only");
   if (qkv_dtype != HKV_DTYPE_BF16 || v_dtype != HKV_DTYPE_BF16)
     return fail(HKV_ERR_UNSUPPORTED, "qkv producer takes a bfloat16 projection and writes bfloat16 v");
-  if (elem_bytes(q_dtype) == 0 || q_dtype != k_dtype)
-    return fail(HKV_ERR_UNSUPPORTED, "q and k outputs must share one dtype: float32, float16 or bfloat16");
+  const bool split_k = k_dtype == HKV_DTYPE_SPLIT_ROWS;
+  if (split_k ? q_dtype != HKV_DTYPE_F32 : (elem_bytes(q_dtype) == 0 || q_dtype != k_dtype))
+    return fail(HKV_ERR_UNSUPPORTED,
+                "q and k outputs must share one dtype: float32, float16 or bfloat16 (or float32 q with k as "
+                "split rows)");
   if (batch < 0 || heads <= 0 || len < 0)
     return fail(HKV_ERR_INVALID_ARG, "batch, len must be >= 0 and heads > 0 (got %d, %d, %d)", batch,
                 len, heads);

@@ -71,7 +71,21 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 template <int DT>
 __device__ __forceinline__ void store_row8(void* base, int64_t elem, const float (&x)[kPer]) {
-  if constexpr (DT == kF32) {
+  if constexpr (DT == kSplitRows) {
+    // split row (hkv_split_rows' format, 512 bytes like an fp32 row): the
+    // 128 bf16 high parts hi = bf16(x), then the 128 low parts bf16(x - hi)
+    u32x4_t hi, lo;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      hi[k] = pack_bf16x2(x[2 * k], x[2 * k + 1]);
+      const float h0 = __builtin_bit_cast(float, hi[k] << 16);
+      const float h1 = __builtin_bit_cast(float, hi[k] & 0xffff0000u);
+      lo[k] = pack_bf16x2(x[2 * k] - h0, x[2 * k + 1] - h1);
+    }
+    uint8_t* const row = static_cast<uint8_t*>(base) + (elem / kD) * (kD * 4) + (elem % kD) * 2;
+    *reinterpret_cast<u32x4_t*>(row) = hi;
+    *reinterpret_cast<u32x4_t*>(row + kD * 2) = lo;
+  } else if constexpr (DT == kF32) {
     f32x4_t* p = reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + elem);
     p[0] = f32x4_t{x[0], x[1], x[2], x[3]};
     p[1] = f32x4_t{x[4], x[5], x[6], x[7]};
@@ -201,6 +215,11 @@ hipError_t launch_produce(const ProduceArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<uint32_t>(blocks));
+  if (a.k_dtype == kSplitRows) {
+    if (a.q_dtype != kF32) return hipErrorInvalidValue;
+    produce_kernel<kF32, kSplitRows><<<grid, kThreads, 0, stream>>>(a);
+    return hipGetLastError();
+  }
   if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
   switch (a.q_dtype) {
     case kF32: produce_kernel<kF32><<<grid, kThreads, 0, stream>>>(a); break;

@@ -159,6 +159,7 @@ def qkv_produce(
     eps: float = 1e-12,
     qk_dtype: torch.dtype = torch.float32,
     append: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
+    k_split_rows: bool = False,
 ):
     """Attention-ready ``q, k, v`` ``[B, H, L, D]`` of one scale from the QKV
     projection output ``qkv`` (bf16 ``[B, L, 3 * H * D]`` or ``[B, L, 3, H, D]``).
@@ -175,7 +176,12 @@ def qkv_produce(
     q, k are ``qk_dtype``: fp32 like the reference, fp16 (the 11-bit
     significand of the TF32 products the reference's attention takes of fp32
     q/k, for values within fp16's range, e.g. cosine attention's), or bf16;
-    v is bf16.
+    v is bf16.  ``k_split_rows`` (fp32 only): k's rows (and the appended slab
+    rows) hold the split rows of the fp32 values instead (the 128 bf16 high
+    parts ``bf16(x)``, then the 128 low parts ``bf16(x - hi)``, 512 bytes like
+    an fp32 row; the tensor keeps dtype float32 so byte copies of it stay
+    valid), the K format the attention's split-row kernel reads: calls with
+    ``k_split_rows=True`` then skip their own split.
     """
     if not qkv.is_cuda:
         raise RuntimeError("qkv_produce runs on the GPU only (HIP kernel); got a CPU tensor")
@@ -196,6 +202,8 @@ def qkv_produce(
         raise ValueError("qkv must be [B, L, 3*H*D] or [B, L, 3, H, D]")
     if qk_dtype not in (torch.float32, torch.float16, torch.bfloat16):
         raise ValueError("qk_dtype must be torch.float32, torch.float16 or torch.bfloat16")
+    if k_split_rows and qk_dtype != torch.float32:
+        raise ValueError("k_split_rows needs qk_dtype=torch.float32")
     qkv = qkv.contiguous()
     dev = qkv.device
     _lib.require_device(dev)
@@ -229,7 +237,8 @@ def qkv_produce(
         qkv.data_ptr(), 3 * H * D, _ptr(qb), _ptr(vb), _ptr(sm), _ptr(rope_table), rope_rows,
         int(rope_start_row), q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(slab_k), _ptr(slab_v),
         _ptr(offsets), capacity, B, H, L, D, _lib.dtype_code(torch.bfloat16), _lib.dtype_code(qk_dtype),
-        _lib.dtype_code(qk_dtype), _lib.dtype_code(torch.bfloat16), 1 if normalize else 0,
+        _lib.DTYPE_SPLIT_ROWS if k_split_rows else _lib.dtype_code(qk_dtype), _lib.dtype_code(torch.bfloat16),
+        1 if normalize else 0,
         float(eps), _lib.stream_handle(dev))
     _lib.check(code)
     return q, k, v

@@ -136,14 +136,31 @@ def _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int) -
             and qk_mode != 2 and value_mode != 2)
 
 
-def attention_queries_per_item(q_dtype, k_dtype, v_dtype) -> int:
+def split_rows_k_format(q_dtype, k_dtype, v_dtype) -> bool:
+    """Whether fp32 K for these dtypes at the current dot-mode knobs goes to
+    the split-row kernel, i.e. whether a producer may write K as split rows
+    (``qkv_produce(..., k_split_rows=True)``) for calls with
+    ``k_split_rows=True``."""
+    return _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(), _fused_value_dot_mode_id())
+
+
+def _check_split_rows_k(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int) -> None:
+    if not (q_dtype == torch.float32 and k_dtype == torch.float32 and v_dtype in (torch.float16, torch.bfloat16)):
+        raise ValueError("k_split_rows takes float32 q, float32-typed K holding split rows and 16-bit v")
+    if qk_mode == 2 or value_mode == 2:
+        raise ValueError("k_split_rows: split K rows feed the split-row kernel, which runs the default and "
+                         "tf32 dot modes only (REAL_PRUNING_FUSED_QK_DOT_MODE / VALUE_DOT_MODE = fp32 need "
+                         "float32 K)")
+
+
+def attention_queries_per_item(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool = False) -> int:
     """Queries per work item of the kernel that :func:`fused_real_pruning_flat_segmented_attention`
     runs for these dtypes at the current dot-mode knobs (the ``queries_per_item``
     of :func:`segmented_attention_plan`), as the library reports it
     (``hkv_segmented_attention_item_shape``): 128, or 256 for the 8-wave form
     of the split-row kernel."""
     qk_mode, value_mode = _fused_qk_dot_mode_id(), _fused_value_dot_mode_id()
-    if not _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode, value_mode):
+    if not (k_split_rows or _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode, value_mode)):
         return 128
     n = int(_lib.load().hkv_segmented_attention_item_shape(
         _lib.dtype_code(q_dtype), _lib.DTYPE_SPLIT_ROWS, _lib.dtype_code(v_dtype), 1, qk_mode, value_mode, 0, None))
@@ -151,11 +168,13 @@ def attention_queries_per_item(q_dtype, k_dtype, v_dtype) -> int:
     return n
 
 
-def attention_fuses_append(q_dtype, k_dtype, v_dtype) -> bool:
+def attention_fuses_append(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool = False) -> bool:
     """Whether :func:`fused_real_pruning_flat_segmented_attention` takes
-    ``append_offsets`` for these dtypes at the current dot-mode knobs (every
-    path but the split-row one, whose slab K is a split copy)."""
-    return not _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(), _fused_value_dot_mode_id())
+    ``append_offsets`` for these dtypes at the current dot-mode knobs: every
+    path but the one that splits fp32 K itself (its slab K is a split copy);
+    K already in split rows (``k_split_rows``) takes it."""
+    return k_split_rows or not _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(),
+                                                _fused_value_dot_mode_id())
 
 
 def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
@@ -292,6 +311,7 @@ def fused_real_pruning_flat_segmented_attention(
     out_dtype: Optional[torch.dtype] = None,
     work_plan: Optional[torch.Tensor] = None,
     append_offsets: Optional[torch.Tensor] = None,
+    k_split_rows: bool = False,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
 
@@ -308,6 +328,10 @@ def fused_real_pruning_flat_segmented_attention(
     ``append_offsets[h]`` (-1: not written) -- the append that follows the
     attention in the reference's cache update, for rows outside every segment
     this call reads (:func:`attention_fuses_append` says which inputs take it).
+    ``k_split_rows`` (an extension): q is fp32 and ``current_k`` /
+    ``persisted_k`` are float32-typed tensors whose rows hold split rows of
+    fp32 K (:func:`qkv_produce` with ``k_split_rows=True``), so the call skips
+    its own split of K; same results as passing the fp32 K.
     Mirrors fused_real_pruning_flat_segmented_attention
     (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
     ``hkv_segmented_attention``.
@@ -400,20 +424,22 @@ def fused_real_pruning_flat_segmented_attention(
         if return_lse
         else None
     )
-    split = _split_rows_path(q.dtype, current_k.dtype, current_v.dtype, qk_mode, value_mode)
+    if k_split_rows:
+        _check_split_rows_k(q.dtype, current_k.dtype, current_v.dtype, qk_mode, value_mode)
+    split = k_split_rows or _split_rows_path(q.dtype, current_k.dtype, current_v.dtype, qk_mode, value_mode)
     if work_plan is not None:
         if (work_plan.dtype != torch.int32 or work_plan.ndim != 2 or work_plan.shape[1] != PLAN_INTS
                 or not work_plan.is_contiguous()):
             raise ValueError(f"work_plan must be a contiguous int32 tensor [units, {PLAN_INTS}]")
         if work_plan.device != q.device:
             raise ValueError("work_plan must be on the same device as q")
-        want = attention_queries_per_item(q.dtype, current_k.dtype, current_v.dtype)
+        want = attention_queries_per_item(q.dtype, current_k.dtype, current_v.dtype, k_split_rows=k_split_rows)
         have = getattr(work_plan, "hkv_queries_per_item", want)
         if have != want:
             raise ValueError(f"work_plan was built for {have}-query items; this call's kernel takes {want} "
                              "(segmented_attention_plan(..., queries_per_item=attention_queries_per_item(...)))")
     if append_offsets is not None:
-        if split:
+        if split and not k_split_rows:
             raise ValueError("append_offsets: the split-row K path writes a split copy of the slab; "
                              "append after the call (attention_fuses_append)")
         if (append_offsets.dtype != torch.int32 or tuple(append_offsets.shape) != (num_heads,)
@@ -427,8 +453,9 @@ def fused_real_pruning_flat_segmented_attention(
     k_code = _lib.dtype_code(current_k.dtype)
     if split:
         # fp32 K as split rows for the split-row kernel (the q split happens in it)
-        persisted_k = _split_rows(persisted_k, stream)
-        current_k = _split_rows(current_k, stream)
+        if not k_split_rows:
+            persisted_k = _split_rows(persisted_k, stream)
+            current_k = _split_rows(current_k, stream)
         k_code = _lib.DTYPE_SPLIT_ROWS
     args = (
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),

@@ -113,6 +113,9 @@ class SegmentedLayerCache:
         self.cached_v: Optional[torch.Tensor] = None
         self.logical_len = 0
         self.active = False  # cached_k/v hold the slab
+        # K rows held as split rows (float32-typed; qkv_produce(k_split_rows=True)),
+        # fixed by the first step after a reset
+        self.k_split_rows = False
 
     def _ensure_slab(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> None:
         """Slab K/V ``[B, capacity, D]`` (:1092-1144); contents of unowned rows are undefined."""
@@ -213,7 +216,7 @@ class SegmentedLayerCache:
 
     def _attend_dense(self, q, k, v, scale, mode, out_dtype=None):
         B, H, L, D = q.shape
-        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype)
+        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows)
         if self.cached_k is None or self.logical_len == 0:
             tables = self._empty_tables(H, q.device, B, L, qpi)
             slab_k = slab_v = None
@@ -225,7 +228,8 @@ class SegmentedLayerCache:
         return fused_real_pruning_flat_segmented_attention(
             q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=tables[0],
             segment_ends=tables[1], segment_counts=tables[2], current_k=k, current_v=v,
-            softmax_scale=scale, softmax_mode=mode, out_dtype=out_dtype, work_plan=tables[3])
+            softmax_scale=scale, softmax_mode=mode, out_dtype=out_dtype, work_plan=tables[3],
+            k_split_rows=self.k_split_rows)
 
     # ------------------------------------------------------------------ step
 
@@ -246,7 +250,8 @@ class SegmentedLayerCache:
 
     def _fused_append_offsets(self, scale_ind: int, q, k, v) -> Optional[torch.Tensor]:
         """``append_offsets`` of this step's attention launch, or None."""
-        if not fused_append_enabled() or not attention_fuses_append(q.dtype, k.dtype, v.dtype):
+        if not fused_append_enabled() or not attention_fuses_append(q.dtype, k.dtype, v.dtype,
+                                                                    k_split_rows=self.k_split_rows):
             return None
         if self.cached_k.dtype != k.dtype or self.cached_v.dtype != v.dtype:
             return None
@@ -255,14 +260,22 @@ class SegmentedLayerCache:
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale_ind: int,
              softmax_scale: float, softmax_mode: Optional[str] = None, appended: bool = False,
-             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+             out_dtype: Optional[torch.dtype] = None, k_split_rows: bool = False) -> torch.Tensor:
         """Attention of scale ``scale_ind`` and the cache update for the next scale.
 
         ``appended``: the producer already wrote the rows offered by
         :meth:`producer_append` for this scale; only the other heads are copied.
-        ``out_dtype``: element type of the output (q's by default)."""
+        ``out_dtype``: element type of the output (q's by default).
+        ``k_split_rows``: k (fp32-typed) holds split rows of fp32 K
+        (``qkv_produce(..., k_split_rows=True)``); every step of a generation
+        passes the same value, and the cache's K rows keep that format."""
         if appended and not self.active:
             raise RuntimeError("appended=True needs an active slab (see producer_append)")
+        if self.logical_len == 0:
+            self.k_split_rows = bool(k_split_rows)
+        elif bool(k_split_rows) != self.k_split_rows:
+            raise ValueError("k_split_rows must be the same for every step of a generation "
+                             f"(cache holds {'split' if self.k_split_rows else 'plain'} K rows)")
         mode = fused_softmax_mode() if softmax_mode is None else softmax_mode
         final = scale_ind + 1 >= self.num_scales
         old_len = self.logical_len
@@ -308,7 +321,8 @@ class SegmentedLayerCache:
                 plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]),
                                                        build=not _capturing(),
                                                        queries_per_item=attention_queries_per_item(
-                                                           q.dtype, k.dtype, v.dtype))
+                                                           q.dtype, k.dtype, v.dtype,
+                                                           k_split_rows=self.k_split_rows))
                         if work_plans_enabled(q.device) else None)
                 offsets = None if final or appended else self._fused_append_offsets(scale_ind, q, k, v)
                 fused = offsets is not None
@@ -317,7 +331,8 @@ class SegmentedLayerCache:
                     q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
                     segment_starts=starts, segment_ends=ends, segment_counts=counts,
                     current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
-                    out_dtype=out_dtype, work_plan=plan, append_offsets=offsets)
+                    out_dtype=out_dtype, work_plan=plan, append_offsets=offsets,
+                    k_split_rows=self.k_split_rows)
 
         with prof.phase("compact"):
             if final:

@@ -301,9 +301,14 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
  *   q_out, k_out : [batch, heads, len, 128] of q_dtype == k_dtype: float32
  *          (the reference's values under autocast), float16 (the same
  *          11-bit significand as the TF32 products the reference's attention
- *          takes of fp32 q/k; elements beyond +-65504 become inf) or bfloat16
+ *          takes of fp32 q/k; elements beyond +-65504 become inf) or bfloat16;
+ *          or float32 q with k_dtype HKV_DTYPE_SPLIT_ROWS: each k row as the
+ *          split row hkv_split_rows writes of the float32 row (512 bytes), the
+ *          K format of the split-row attention kernel, so attention calls on
+ *          these rows need no split of their own
  *   v_out : bf16 [batch, heads, len, 128]
- *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / bf16
+ *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / bf16 (split
+ *          rows: 512-byte rows)
  *   append_offsets : NULL or int32 [heads] (-1 = head not appended)
  * All pointers 16-byte aligned.  Rows (b, l, h) with append_offsets[h] + l
  * outside [0, slab_capacity) are not appended.

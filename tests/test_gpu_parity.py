@@ -465,6 +465,66 @@ def test_attention_random_shapes_split_rows(seed, device, monkeypatch):
         _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan_other)
 
 
+def test_attention_k_split_rows_matches_fp32_k(device):
+    """The operator on K given as split rows (k_split_rows=True, as the
+    producer writes it) against the same call on fp32 K (split by the call
+    itself): outputs and LSE bit-identical; the fused append on split rows
+    writes the split rows; the wrong dtypes or an fp32 dot mode are refused."""
+    from heatkv_amd.real_pruning_fused_attention import _split_rows
+
+    g = torch.Generator().manual_seed(31)
+    B, H, L, cap = 2, 5, 200, 700
+    stream = torch.cuda.current_stream(device)
+    split = lambda t: _split_rows(t.contiguous(), stream).view(torch.float32)  # noqa: E731
+    q = (torch.nn.functional.normalize(torch.randn((B, H, L, 128), generator=g), dim=-1) * 30).to(device)
+    ck = torch.nn.functional.normalize(torch.randn((B, H, L, 128), generator=g), dim=-1).to(device)
+    cv = torch.randn((B, H, L, 128), generator=g).to(torch.bfloat16).to(device)
+    sk = torch.nn.functional.normalize(torch.randn((B, cap, 128), generator=g), dim=-1).to(device)
+    sv = torch.randn((B, cap, 128), generator=g).to(torch.bfloat16).to(device)
+    st = torch.tensor([[0, 100, 0], [150, 0, 0], [0, 0, 0], [300, 400, 500], [10, 0, 0]], dtype=torch.int32)
+    en = torch.tensor([[64, 140, 0], [151, 0, 0], [0, 0, 0], [380, 420, 600], [12, 0, 0]], dtype=torch.int32)
+    ct = torch.tensor([2, 1, 0, 3, 1], dtype=torch.int32)
+    tables = dict(segment_starts=st.to(device), segment_ends=en.to(device), segment_counts=ct.to(device))
+    kw = dict(q=q, persisted_v=sv, current_v=cv, softmax_scale=1.0, return_lse=True, **tables)
+    out_f, lse_f = fused_real_pruning_flat_segmented_attention(persisted_k=sk, current_k=ck, **kw)
+    out_s, lse_s = fused_real_pruning_flat_segmented_attention(persisted_k=split(sk), current_k=split(ck),
+                                                               k_split_rows=True, **kw)
+    torch.cuda.synchronize(device)
+    assert torch.equal(out_f, out_s) and torch.equal(lse_f, lse_s)
+    # the append of 50 current rows of heads 1 and 3 into slab rows [600, 650)
+    # and [650, 700) (outside every segment the call reads)
+    offs = torch.tensor([-1, 600, -1, 650, -1], dtype=torch.int32, device=device)
+    slab_k = split(sk).clone()
+    slab_v = sv.clone()
+    n = 50
+    fused_real_pruning_flat_segmented_attention(
+        q=q[:, :, :n].contiguous(), persisted_k=slab_k, persisted_v=slab_v, current_k=split(ck[:, :, :n]),
+        current_v=cv[:, :, :n].contiguous(), softmax_scale=1.0, k_split_rows=True, append_offsets=offs,
+        **tables)
+    torch.cuda.synchronize(device)
+    want_k, want_v = split(sk).clone(), sv.clone()
+    for h, off in ((1, 600), (3, 650)):
+        want_k[:, off:off + n] = split(ck[:, h, :n])
+        want_v[:, off:off + n] = cv[:, h, :n]
+    assert torch.equal(slab_k, want_k) and torch.equal(slab_v, want_v)
+    with pytest.raises(ValueError, match="k_split_rows"):
+        fused_real_pruning_flat_segmented_attention(persisted_k=split(sk).bfloat16(), current_k=ck.bfloat16(),
+                                                    k_split_rows=True, **dict(kw, q=q.bfloat16()))
+
+
+def test_attention_k_split_rows_refuses_fp32_dot_mode(device, monkeypatch):
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "fp32")
+    B, H, L = 1, 2, 64
+    q = torch.randn((B, H, L, 128), device=device)
+    v = torch.randn((B, H, L, 128), device=device).bfloat16()
+    z = torch.zeros((H, 0), dtype=torch.int32, device=device)
+    c = torch.zeros((H,), dtype=torch.int32, device=device)
+    with pytest.raises(ValueError, match="dot modes"):
+        fused_real_pruning_flat_segmented_attention(q=q, persisted_k=None, persisted_v=None, segment_starts=z,
+                                                    segment_ends=z, segment_counts=c, current_k=q, current_v=v,
+                                                    softmax_scale=1.0, k_split_rows=True)
+
+
 def test_split_rows_bit_exact(device):
     """hkv_split_rows against the split restated in numpy: hi = x rounded to
     bf16 (nearest even), lo = (x - hi) rounded to bf16 (x - hi is exact in

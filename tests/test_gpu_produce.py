@@ -194,6 +194,86 @@ def test_generation_with_fused_append_matches_unfused(device):
     assert n_fused >= 3
 
 
+def _split(t: torch.Tensor) -> torch.Tensor:
+    """hkv_split_rows of fp32 rows, viewed as float32 (the producer's split-row K form)."""
+    from heatkv_amd.real_pruning_fused_attention import _split_rows
+
+    return _split_rows(t.contiguous(), torch.cuda.current_stream(t.device)).view(torch.float32)
+
+
+def test_producer_split_rows_k(device):
+    """qkv_produce(k_split_rows=True): k's rows (and the appended slab rows)
+    are bit for bit hkv_split_rows of the fp32 k the producer writes without
+    it; q and v unchanged; slab rows not appended untouched."""
+    B, L, H, cap = 2, 144, 6, 1000
+    qkv = _qkv(B, L, H, 17).to(device)
+    sm = _scale_mul(H, 18).to(device)
+    table = P.rope2d_freqs_table(D, SCHED_1M, 2, 128).to(device)
+    start = P.rope_start(SCHED_1M, 5)
+    slab_k = torch.full((B, cap, D), 7.5, device=device)
+    slab_v = torch.full((B, cap, D), -3.25, device=device, dtype=torch.bfloat16)
+    offs = torch.tensor([0, -1, 500, 900, -1, 144], dtype=torch.int32, device=device)
+    q, k, v = P.qkv_produce(qkv, H, scale_mul=sm, rope_table=table, rope_start_row=start,
+                            append=(slab_k, slab_v, offs), k_split_rows=True)
+    q2, k2, v2 = P.qkv_produce(qkv, H, scale_mul=sm, rope_table=table, rope_start_row=start)
+    ks = _split(k2)
+    torch.cuda.synchronize(device)
+    assert k.dtype == torch.float32 and tuple(k.shape) == (B, H, L, D)
+    assert torch.equal(q, q2) and torch.equal(v, v2)
+    assert np.array_equal(bits(k), bits(ks))
+    sk = bits(slab_k)
+    written = np.zeros(cap, bool)
+    for h, off in enumerate(offs.tolist()):
+        if off < 0:
+            continue
+        n = min(L, cap - off)
+        assert np.array_equal(sk[:, off:off + n], bits(ks[:, h, :n])), h
+        written[off:off + n] = True
+    assert np.all(to_np(slab_k)[:, ~written] == 7.5)
+    with pytest.raises(ValueError, match="k_split_rows"):
+        P.qkv_produce(qkv, H, qk_dtype=torch.bfloat16, k_split_rows=True)
+
+
+def test_generation_split_rows_k_matches_fp32_k(device):
+    """13-scale generation (B=2, H=16) under orders/2b.json at budget 0.1 at
+    the model's precision (fp32 q/k): the producer writing K as split rows
+    (k_split_rows, the cache keeping them; appends fused into the producer
+    and the attention launch) gives outputs bit-identical to fp32 K split on
+    every call, and every live slab K row is the split of the fp32 path's."""
+    orders = json.load(open(os.path.join(HERE, "golden", "orders_2b.json")))
+    ctrl = POL.controller_for_budget(0.1, orders, num_layers=32, num_heads=16, protected_prefix_scales=3)
+    layer, H, B = 29, 16, 2
+    sched = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
+    removed = lambda t: ctrl.removed_heads_by_source_for(layer, t)  # noqa: E731
+    split = sc.SegmentedLayerCache(sched, removed, num_heads=H)
+    plain = sc.SegmentedLayerCache(sched, removed, num_heads=H)
+    table = P.rope2d_freqs_table(D, SCHED_1M, 2, 128).to(device)
+    sm = _scale_mul(H, 19).to(device)
+    for t, side in enumerate(SIDES_1M):
+        qkv = _qkv(B, side * side, H, 2000 + t).to(device)
+        start = P.rope_start(SCHED_1M, t)
+        app = split.producer_append(t, torch.float32, device)
+        q, k, v = P.qkv_produce(qkv, H, scale_mul=sm, rope_table=table, rope_start_row=start, append=app,
+                                k_split_rows=True)
+        out_s = split.step(q, k, v, t, 1.0, appended=app is not None, k_split_rows=True)
+        q2, k2, v2 = P.qkv_produce(qkv, H, scale_mul=sm, rope_table=table, rope_start_row=start)
+        out_p = plain.step(q2, k2, v2, t, 1.0)
+        torch.cuda.synchronize(device)
+        print(f"[split-row K] step {t} producer append {app is not None}", flush=True)
+        assert torch.equal(out_s, out_p), t
+        if split.active and t + 1 < len(SIDES_1M):
+            for seg in sched.live_segments(t + 1):
+                rows = slice(seg.offset, seg.offset + seg.length)
+                assert torch.equal(split.cached_k[:, rows], _split(plain.cached_k[:, rows])), (t, seg)
+                assert torch.equal(split.cached_v[:, rows], plain.cached_v[:, rows]), (t, seg)
+    # a generation keeps one K format
+    steps = [P.qkv_produce(_qkv(B, side * side, H, 3000 + t).to(device), H, scale_mul=sm, k_split_rows=True)
+             for t, side in enumerate(SIDES_1M[:2])]
+    split.step(*steps[0], 0, 1.0, k_split_rows=True)
+    with pytest.raises(ValueError, match="same for every step"):
+        split.step(*steps[1], 1, 1.0, k_split_rows=False)
+
+
 @pytest.mark.parametrize("budget,qk_mode", [(1.0, "bf16"), (0.3, "bf16"), (0.3, "tf32")])
 @torch.no_grad()
 def test_patched_layer_forward(device, budget, qk_mode, monkeypatch):
