@@ -583,16 +583,30 @@ def _host_slab(wl):
 
 
 def _cpu_model():
+    """The host CPU as lscpu names it, with its family / model / stepping (a
+    virtual machine may report a short model name such as "AMD EPYC")."""
     import subprocess
 
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            fields[key.strip()] = val.strip()
     except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    if "Model name" not in fields:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        fields["Model name"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    name = fields.get("Model name", "unknown")
+    ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k)]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_baseline(wl, repeats):

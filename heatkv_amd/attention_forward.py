@@ -104,14 +104,15 @@ def real_scale_fused_segmented_forward(self, x, attn_bias_or_two_vector=None, at
         start = rope_start(scale_schedule, scale_ind)
     cos_attn = bool(self.cos_attn)
     # q and k are fp32 wherever the reference promotes them (cosine attention
-    # or RoPE); otherwise they stay bf16 as in the reference.  TF32 dot mode
+    # or RoPE); otherwise they keep the projection's dtype as in the
+    # reference (bf16 under its bf16 autocast).  TF32 dot mode
     # on a cosine-attention layer: fp16 (TF32's significand, values in range).
-    qk_dtype = torch.float32 if (cos_attn or table is not None) else torch.bfloat16
+    qk_dtype = torch.float32 if (cos_attn or table is not None) else qkv.dtype
     if cos_attn and _fused_qk_dot_mode_id() == _QK_DOT_TF32:
         qk_dtype = torch.float16
     # fp32 K that the attention reads as split rows is written in that form
     # by the producer (and kept so in the cache), so no call splits it again
-    k_split = split_rows_k_format(qk_dtype, qk_dtype, torch.bfloat16)
+    k_split = split_rows_k_format(qk_dtype, qk_dtype, qkv.dtype)
     cache = self.heatkv_cache
     append = cache.producer_append(int(scale_ind), qk_dtype, qkv.device)
     q, k, v = qkv_produce(

@@ -298,8 +298,10 @@ int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bi
                         int32_t head_dim, int32_t qkv_dtype, int32_t q_dtype, int32_t k_dtype,
                         int32_t v_dtype, int32_t normalize, float eps, void* stream) {
   if (head_dim != 128) return fail(HKV_ERR_UNSUPPORTED, "qkv producer supports head_dim=128 only");
-  if (qkv_dtype != HKV_DTYPE_BF16 || v_dtype != HKV_DTYPE_BF16)
-    return fail(HKV_ERR_UNSUPPORTED, "qkv producer takes a bfloat16 projection and writes bfloat16 v");
+  if (elem_bytes(qkv_dtype) == 0 || v_dtype != qkv_dtype)
+    return fail(HKV_ERR_UNSUPPORTED,
+                "qkv producer takes a bfloat16, float16 or float32 projection and writes v in its dtype "
+                "(got projection %d, v %d)", qkv_dtype, v_dtype);
   const bool split_k = k_dtype == HKV_DTYPE_SPLIT_ROWS;
   if (split_k ? q_dtype != HKV_DTYPE_F32 : (elem_bytes(q_dtype) == 0 || q_dtype != k_dtype))
     return fail(HKV_ERR_UNSUPPORTED,
@@ -344,6 +346,7 @@ int32_t hkv_qkv_produce(const void* qkv, int64_t token_stride, const float* q_bi
   a.rows = static_cast<int64_t>(batch) * len * heads;
   a.heads = heads;
   a.len = len;
+  a.qkv_dtype = qkv_dtype;
   a.q_dtype = q_dtype;
   a.k_dtype = k_dtype;
   a.normalize = normalize != 0;

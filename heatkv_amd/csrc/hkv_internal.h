@@ -118,7 +118,7 @@ int64_t split_workspace_bytes(int32_t slots);
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream);
 
 struct ProduceArgs {
-  const void* qkv;            // bf16 [B, L, 3, H, D], token stride in elements
+  const void* qkv;            // [B, L, 3, H, D] of qkv_dtype, token stride in elements
   int64_t token_stride;
   const float* q_bias;        // [H * D] or null
   const float* v_bias;        // [H * D] or null
@@ -128,14 +128,15 @@ struct ProduceArgs {
   int64_t rope_start;         // table row of token 0
   void* q_out;                // [B, H, L, D], q_dtype
   void* k_out;                // [B, H, L, D], k_dtype
-  void* v_out;                // [B, H, L, D], bf16
+  void* v_out;                // [B, H, L, D], qkv_dtype
   void* slab_k;               // [B, slab_capacity, D], k_dtype (append) or null
-  void* slab_v;               // [B, slab_capacity, D], bf16
+  void* slab_v;               // [B, slab_capacity, D], qkv_dtype
   const int32_t* append_offsets;  // [H], -1 = head not appended; null = no append
   int64_t slab_capacity;
   int64_t rows;               // B * L * H
   int32_t heads;
   int32_t len;
+  int32_t qkv_dtype;          // the projection's element type, also v's
   int32_t q_dtype;
   int32_t k_dtype;
   int32_t normalize;

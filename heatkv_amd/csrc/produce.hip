@@ -143,8 +143,45 @@ __device__ __forceinline__ void rotate(float (&x)[kPer], f32x4_t c, f32x4_t s) {
   }
 }
 
-template <int QT, int KT = QT>
+// 8 elements of the projection (element type IT) at `p` as floats; the raw
+// bytes (16 for 16-bit types, 32 for fp32) in `raw` for a copy that keeps them.
+template <int IT>
+__device__ __forceinline__ void load_row8(const uint8_t* p, float (&x)[kPer], u32x4_t (&raw)[2]) {
+  raw[0] = *reinterpret_cast<const u32x4_t*>(p);
+  if constexpr (IT == kF32) {
+    raw[1] = *reinterpret_cast<const u32x4_t*>(p + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = __uint_as_float(raw[0][i]);
+      x[4 + i] = __uint_as_float(raw[1][i]);
+    }
+  } else if constexpr (IT == kF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(raw[0][i] & 0xffffu)));
+      x[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(raw[0][i] >> 16)));
+    }
+  } else {
+    unpack_bf16x8(raw[0], x);
+  }
+}
+
+template <int IT>
+__device__ __forceinline__ void store_raw8(void* base, int64_t elem, const u32x4_t (&raw)[2]) {
+  if constexpr (IT == kF32) {
+    u32x4_t* p = reinterpret_cast<u32x4_t*>(static_cast<float*>(base) + elem);
+    p[0] = raw[0];
+    p[1] = raw[1];
+  } else {
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(base) + elem) = raw[0];
+  }
+}
+
+// IT: the projection's element type (bf16, fp16 or fp32), also v's; QT, KT:
+// the q and k outputs' (KT kSplitRows: k as split rows).
+template <int IT, int QT, int KT = QT>
 __global__ __launch_bounds__(kThreads) void produce_kernel(ProduceArgs a) {
+  constexpr int kElem = IT == kF32 ? 4 : 2;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
   const int j = threadIdx.x % kLanes;
   // Whole 16-lane rows leave together, so the row reductions stay complete.
@@ -155,11 +192,13 @@ __global__ __launch_bounds__(kThreads) void produce_kernel(ProduceArgs a) {
   const int64_t b = tok / a.len;
   const int64_t hd = static_cast<int64_t>(a.heads) * kD;
 
-  const uint16_t* src = static_cast<const uint16_t*>(a.qkv) + tok * a.token_stride +
-                        static_cast<int64_t>(h) * kD + j * kPer;
-  const u32x4_t wq = *reinterpret_cast<const u32x4_t*>(src);
-  const u32x4_t wk = *reinterpret_cast<const u32x4_t*>(src + hd);
-  u32x4_t wv = *reinterpret_cast<const u32x4_t*>(src + 2 * hd);
+  const uint8_t* src = static_cast<const uint8_t*>(a.qkv) +
+                       (tok * a.token_stride + static_cast<int64_t>(h) * kD + j * kPer) * kElem;
+  float q[kPer], k[kPer], v[kPer];
+  u32x4_t rq[2], rk[2], rv[2];
+  load_row8<IT>(src, q, rq);
+  load_row8<IT>(src + hd * kElem, k, rk);
+  load_row8<IT>(src + 2 * hd * kElem, v, rv);
   f32x4_t rc = {1.f, 1.f, 1.f, 1.f}, rs = {0.f, 0.f, 0.f, 0.f};
   if (a.rope != nullptr) {
     const int64_t pos = a.rope_start + l;
@@ -167,18 +206,8 @@ __global__ __launch_bounds__(kThreads) void produce_kernel(ProduceArgs a) {
     rs = *reinterpret_cast<const f32x4_t*>(a.rope + (a.rope_rows + pos) * (kD / 2) + j * 4);
   }
 
-  float q[kPer], k[kPer];
-  unpack_bf16x8(wq, q);
-  unpack_bf16x8(wk, k);
   const int64_t bias_off = static_cast<int64_t>(h) * kD + j * kPer;
   if (a.q_bias != nullptr) add_bias(q, a.q_bias + bias_off);
-  if (a.v_bias != nullptr) {
-    float v[kPer];
-    unpack_bf16x8(wv, v);
-    add_bias(v, a.v_bias + bias_off);
-    wv = u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                 pack_bf16x2(v[6], v[7])};
-  }
   if (a.normalize) {
     normalize(q, a.eps);
     normalize(k, a.eps);
@@ -196,16 +225,41 @@ __global__ __launch_bounds__(kThreads) void produce_kernel(ProduceArgs a) {
   const int64_t orow = ((b * a.heads + h) * a.len + l) * kD + j * kPer;
   store_row8<QT>(a.q_out, orow, q);
   store_row8<KT>(a.k_out, orow, k);
-  *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.v_out) + orow) = wv;
+  // v keeps the projection's values and type (the bias, when given, added in
+  // fp32 and rounded to that type once)
+  if (a.v_bias != nullptr) {
+    add_bias(v, a.v_bias + bias_off);
+    store_row8<IT>(a.v_out, orow, v);
+  } else {
+    store_raw8<IT>(a.v_out, orow, rv);
+  }
 
   if (a.append_offsets != nullptr) {
     const int32_t off = a.append_offsets[h];
     if (off >= 0 && static_cast<int64_t>(off) + l < a.slab_capacity) {
       const int64_t srow = (b * a.slab_capacity + off + l) * kD + j * kPer;
       store_row8<KT>(a.slab_k, srow, k);
-      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.slab_v) + srow) = wv;
+      if (a.v_bias != nullptr) store_row8<IT>(a.slab_v, srow, v);
+      else store_raw8<IT>(a.slab_v, srow, rv);
     }
   }
+}
+
+template <int IT>
+hipError_t launch_for_input(const ProduceArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.k_dtype == kSplitRows) {
+    if (a.q_dtype != kF32) return hipErrorInvalidValue;
+    produce_kernel<IT, kF32, kSplitRows><<<grid, kThreads, 0, stream>>>(a);
+    return hipGetLastError();
+  }
+  if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
+  switch (a.q_dtype) {
+    case kF32: produce_kernel<IT, kF32><<<grid, kThreads, 0, stream>>>(a); break;
+    case kF16: produce_kernel<IT, kF16><<<grid, kThreads, 0, stream>>>(a); break;
+    case kBF16: produce_kernel<IT, kBF16><<<grid, kThreads, 0, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -215,19 +269,12 @@ hipError_t launch_produce(const ProduceArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<uint32_t>(blocks));
-  if (a.k_dtype == kSplitRows) {
-    if (a.q_dtype != kF32) return hipErrorInvalidValue;
-    produce_kernel<kF32, kSplitRows><<<grid, kThreads, 0, stream>>>(a);
-    return hipGetLastError();
-  }
-  if (a.q_dtype != a.k_dtype) return hipErrorInvalidValue;
-  switch (a.q_dtype) {
-    case kF32: produce_kernel<kF32><<<grid, kThreads, 0, stream>>>(a); break;
-    case kF16: produce_kernel<kF16><<<grid, kThreads, 0, stream>>>(a); break;
-    case kBF16: produce_kernel<kBF16><<<grid, kThreads, 0, stream>>>(a); break;
+  switch (a.qkv_dtype) {
+    case kBF16: return launch_for_input<kBF16>(a, grid, stream);
+    case kF16: return launch_for_input<kF16>(a, grid, stream);
+    case kF32: return launch_for_input<kF32>(a, grid, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace hkv

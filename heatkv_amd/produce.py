@@ -7,7 +7,9 @@ and k in fp32 (torch's autocast runs ``norm`` in fp32, so the quotient is
 fp32), multiplies q by ``exp(min(scale_mul, max_scale_mul))`` per head, and
 ``apply_rotary_emb`` (infinity/models/basic.py:97-117) rotates each pair
 ``(2i, 2i+1)`` of q and k by the 2-D RoPE table row of its token.  q and k
-come out fp32 ``[B, H, L, D]``, v bf16.
+come out fp32 ``[B, H, L, D]``, v bf16.  Under fp16 autocast the projection
+is fp16, without autocast fp32; q and k are computed in fp32 the same way and
+v keeps the projection's dtype.
 
 :func:`qkv_produce` runs all of it in one HIP kernel (``hkv_qkv_produce``),
 optionally with the fused QKV bias and with the append of the kept heads'
@@ -162,12 +164,14 @@ def qkv_produce(
     k_split_rows: bool = False,
 ):
     """Attention-ready ``q, k, v`` ``[B, H, L, D]`` of one scale from the QKV
-    projection output ``qkv`` (bf16 ``[B, L, 3 * H * D]`` or ``[B, L, 3, H, D]``).
+    projection output ``qkv`` (``[B, L, 3 * H * D]`` or ``[B, L, 3, H, D]``;
+    bf16 under the reference's bf16 autocast, fp16 under fp16 autocast, fp32
+    without autocast).
 
     * ``scale_mul``: per-head multiplier of q (``[H]``), e.g. :func:`scale_mul_of`;
     * ``rope_table``: ``[2, T, D // 2]`` fp32 device table (cos, sin), rows
       ``rope_start_row ...`` used for the scale's tokens; None skips RoPE;
-    * ``q_bias``, ``v_bias``: ``[H * D]`` biases added in fp32 to the bf16
+    * ``q_bias``, ``v_bias``: ``[H * D]`` biases added in fp32 to the
       projection (leave None when the projection applied them);
     * ``append``: ``(slab_k, slab_v, offsets)`` -- slab ``[B, capacity, D]`` of
       k's / v's dtype and int32 ``[H]`` device offsets (-1 = not appended):
@@ -176,7 +180,7 @@ def qkv_produce(
     q, k are ``qk_dtype``: fp32 like the reference, fp16 (the 11-bit
     significand of the TF32 products the reference's attention takes of fp32
     q/k, for values within fp16's range, e.g. cosine attention's), or bf16;
-    v is bf16.  ``k_split_rows`` (fp32 only): k's rows (and the appended slab
+    v keeps the projection's dtype and values.  ``k_split_rows`` (fp32 only): k's rows (and the appended slab
     rows) hold the split rows of the fp32 values instead (the 128 bf16 high
     parts ``bf16(x)``, then the 128 low parts ``bf16(x - hi)``, 512 bytes like
     an fp32 row; the tensor keeps dtype float32 so byte copies of it stay
@@ -185,9 +189,8 @@ def qkv_produce(
     """
     if not qkv.is_cuda:
         raise RuntimeError("qkv_produce runs on the GPU only (HIP kernel); got a CPU tensor")
-    if qkv.dtype != torch.bfloat16:
-        raise RuntimeError("qkv_produce takes the bfloat16 QKV projection (the reference runs it under "
-                           f"bf16 autocast); got {qkv.dtype}")
+    if qkv.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError(f"qkv_produce takes a bfloat16, float16 or float32 QKV projection; got {qkv.dtype}")
     H = int(num_heads)
     D = HEAD_DIM
     if qkv.dim() == 5:
@@ -209,7 +212,7 @@ def qkv_produce(
     _lib.require_device(dev)
     q = torch.empty((B, H, L, D), device=dev, dtype=qk_dtype)
     k = torch.empty((B, H, L, D), device=dev, dtype=qk_dtype)
-    v = torch.empty((B, H, L, D), device=dev, dtype=torch.bfloat16)
+    v = torch.empty((B, H, L, D), device=dev, dtype=qkv.dtype)
     sm = _vector(scale_mul, H, "scale_mul", dev)
     qb = _vector(q_bias, H * D, "q_bias", dev)
     vb = _vector(v_bias, H * D, "v_bias", dev)
@@ -223,7 +226,7 @@ def qkv_produce(
     capacity = 0
     if append is not None:
         slab_k, slab_v, offsets = append
-        if slab_k.dtype != qk_dtype or slab_v.dtype != torch.bfloat16:
+        if slab_k.dtype != qk_dtype or slab_v.dtype != qkv.dtype:
             raise ValueError("append slabs must have k's and v's dtypes")
         if (slab_k.dim() != 3 or tuple(slab_k.shape) != tuple(slab_v.shape) or int(slab_k.shape[0]) != B
                 or int(slab_k.shape[2]) != D or not slab_k.is_contiguous() or not slab_v.is_contiguous()):
@@ -236,8 +239,8 @@ def qkv_produce(
     code = _lib.load().hkv_qkv_produce(
         qkv.data_ptr(), 3 * H * D, _ptr(qb), _ptr(vb), _ptr(sm), _ptr(rope_table), rope_rows,
         int(rope_start_row), q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(slab_k), _ptr(slab_v),
-        _ptr(offsets), capacity, B, H, L, D, _lib.dtype_code(torch.bfloat16), _lib.dtype_code(qk_dtype),
-        _lib.DTYPE_SPLIT_ROWS if k_split_rows else _lib.dtype_code(qk_dtype), _lib.dtype_code(torch.bfloat16),
+        _ptr(offsets), capacity, B, H, L, D, _lib.dtype_code(qkv.dtype), _lib.dtype_code(qk_dtype),
+        _lib.DTYPE_SPLIT_ROWS if k_split_rows else _lib.dtype_code(qk_dtype), _lib.dtype_code(qkv.dtype),
         1 if normalize else 0,
         float(eps), _lib.stream_handle(dev))
     _lib.check(code)

@@ -290,11 +290,13 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
  * the kept heads' current rows into the slab that the reference runs after
  * attention (enable_real_pruning_fast.py:969-995, 1791-1807).  The append may
  * only be fused when no slab row it writes is read by this scale's attention.
- *   qkv : bf16 [batch, len, 3, heads, 128] with token stride token_stride
- *         elements (>= 3 * heads * 128, multiple of 8)
- *   q_bias, v_bias : NULL or float32 [heads * 128]; added in fp32 to the bf16
+ *   qkv : [batch, len, 3, heads, 128] of qkv_dtype (bf16 under the
+ *         reference's bf16 autocast; fp16 under fp16 autocast; fp32 without
+ *         autocast) with token stride token_stride elements (>= 3 * heads *
+ *         128, multiple of 8)
+ *   q_bias, v_bias : NULL or float32 [heads * 128]; added in fp32 to the
  *         projection output (the reference adds them before the GEMM output
- *         is rounded to bf16)
+ *         is rounded to the projection's type)
  *   scale_mul : NULL or float32 [heads] (the exp of the clamped learned scale)
  *   rope : NULL or float32 [2, rope_rows, 64] (cos table, then sin table);
  *          rows [rope_start, rope_start + len) are used
@@ -306,9 +308,10 @@ int32_t hkv_segmented_attention_noalloc(const void* q, const void* slab_k, const
  *          split row hkv_split_rows writes of the float32 row (512 bytes), the
  *          K format of the split-row attention kernel, so attention calls on
  *          these rows need no split of their own
- *   v_out : bf16 [batch, heads, len, 128]
- *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / bf16 (split
- *          rows: 512-byte rows)
+ *   v_out : [batch, heads, len, 128] of v_dtype == qkv_dtype (the
+ *          projection's values; with v_bias, rounded once to that type)
+ *   slab_k / slab_v : [batch, slab_capacity, 128] of k_dtype / v_dtype
+ *          (split rows: 512-byte rows)
  *   append_offsets : NULL or int32 [heads] (-1 = head not appended)
  * All pointers 16-byte aligned.  Rows (b, l, h) with append_offsets[h] + l
  * outside [0, slab_capacity) are not appended.

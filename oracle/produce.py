@@ -14,7 +14,8 @@ Follows the reference layer forward under bf16 autocast
   its token: ``(c*x0 - s*x1, s*x0 + c*x1)``, each product and sum rounded to
   fp32 separately (elementwise tensor ops, basic.py:110-113);
 * outputs are ``[B, H, L, D]``; v is the bf16 value (plus bias, rounded to
-  bf16 to nearest even).
+  bf16 to nearest even); for an fp16 or fp32 projection (fp16 autocast, no
+  autocast) the same in that type.
 
 ``rope_table`` restates ``precompute_rope2d_freqs_grid`` (basic.py:39-94) for
 one schedule, with the angles in float64.
@@ -125,10 +126,18 @@ def rotate_pairs(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     return out
 
 
+def fp16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest float16 (ties to even), returned as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def produce(qkv: np.ndarray, *, scale_mul=None, table=None, start: int = 0, q_bias=None, v_bias=None,
-            normalize: bool = True, eps: float = 1e-12):
-    """``(q, k, v)`` ``[B, H, L, D]`` (q, k float32; v float32 holding bf16 values)
-    from ``qkv`` ``[B, L, 3, H, D]`` float32 (bf16 values)."""
+            normalize: bool = True, eps: float = 1e-12, v_type: str = "bf16"):
+    """``(q, k, v)`` ``[B, H, L, D]`` (q, k float32; v float32 holding values
+    of the projection's type ``v_type``: "bf16", "fp16" or "fp32") from
+    ``qkv`` ``[B, L, 3, H, D]`` float32 (values of that type); v plus
+    ``v_bias`` is rounded once to that type."""
+    v_round = {"bf16": bf16_round, "fp16": fp16_round, "fp32": lambda a: np.asarray(a, np.float32)}[v_type]
     qkv = np.asarray(qkv, dtype=np.float32)
     B, L, _, H, D = qkv.shape
     q = qkv[:, :, 0].copy()
@@ -137,7 +146,7 @@ def produce(qkv: np.ndarray, *, scale_mul=None, table=None, start: int = 0, q_bi
     if q_bias is not None:
         q = (q + np.asarray(q_bias, np.float32).reshape(H, D)).astype(np.float32)
     if v_bias is not None:
-        v = bf16_round((v + np.asarray(v_bias, np.float32).reshape(H, D)).astype(np.float32))
+        v = v_round((v + np.asarray(v_bias, np.float32).reshape(H, D)).astype(np.float32))
     if normalize:
         q = normalize_rows(q, eps)
         k = normalize_rows(k, eps)

@@ -123,6 +123,43 @@ def test_producer_bias_no_normalize_and_bf16_out(device):
         assert np.all(np.abs(g32 - want) <= np.abs(want) * 2.0 ** -11 + 2.0 ** -25 + atol)
 
 
+@pytest.mark.parametrize("proj", [torch.float16, torch.float32])
+def test_producer_fp16_fp32_projection(device, proj):
+    """fp16 (fp16 autocast) and fp32 (no autocast) projections: q, k against
+    the oracle as for bf16, v keeps the projection's dtype and values
+    (bit-exact; with v_bias rounded once to that dtype), the appended slab
+    rows equal the outputs; fp32 k as split rows is the split of the fp32 k."""
+    B, L, H, cap = 2, 400, 8, 900
+    g = torch.Generator().manual_seed(21)
+    qkv = (torch.randn((B, L, 3 * H * D), generator=g) * 2).to(proj)
+    vb = torch.randn(H * D, generator=g)
+    sm = _scale_mul(H, 22)
+    table = P.rope2d_freqs_table(D, SCHED_1M, 2, 128)
+    start = P.rope_start(SCHED_1M, 9)
+    arr = qkv.float().numpy().reshape(B, L, 3, H, D)
+    vt = "fp16" if proj == torch.float16 else "fp32"
+    slab_k = torch.zeros((B, cap, D), device=device)
+    slab_v = torch.zeros((B, cap, D), device=device, dtype=proj)
+    offs = torch.tensor([0, -1, 400, -1, -1, -1, -1, 850], dtype=torch.int32, device=device)
+    q, k, v = P.qkv_produce(qkv.to(device), H, scale_mul=sm.to(device), rope_table=table.to(device),
+                            rope_start_row=start, v_bias=vb.to(device), append=(slab_k, slab_v, offs))
+    wq, wk, wv = O.produce(arr, scale_mul=sm.numpy(), table=table.numpy(), start=start, v_bias=vb.numpy(),
+                           v_type=vt)
+    assert v.dtype == proj
+    _check_qk(q, k, wq, wk, sm.numpy(), H)
+    assert np.array_equal(to_np(v.float()), wv)
+    for h, off in ((0, 0), (2, 400), (7, 850)):
+        n = min(L, cap - off)
+        assert torch.equal(slab_k[:, off:off + n], k[:, h, :n]) and torch.equal(slab_v[:, off:off + n], v[:, h, :n])
+    # no bias: v is the projection's v, bit for bit
+    _, k2, v2 = P.qkv_produce(qkv.to(device), H, scale_mul=sm.to(device), rope_table=table.to(device),
+                              rope_start_row=start)
+    assert np.array_equal(bits(v2), bits(qkv.reshape(B, L, 3, H, D)[:, :, 2].permute(0, 2, 1, 3).contiguous()))
+    _, ks, _ = P.qkv_produce(qkv.to(device), H, scale_mul=sm.to(device), rope_table=table.to(device),
+                             rope_start_row=start, k_split_rows=True)
+    assert np.array_equal(bits(ks), bits(_split(k2)))
+
+
 def test_producer_zero_rows_5d_input_and_empty(device):
     B, L, H = 1, 16, 2
     qkv = _qkv(B, L, H, 6).reshape(B, L, 3, H, D)
@@ -274,16 +311,19 @@ def test_generation_split_rows_k_matches_fp32_k(device):
         split.step(*steps[1], 1, 1.0, k_split_rows=False)
 
 
-@pytest.mark.parametrize("budget,qk_mode", [(1.0, "bf16"), (0.3, "bf16"), (0.3, "tf32")])
+@pytest.mark.parametrize("budget,qk_mode,amp", [(1.0, "bf16", "bf16"), (0.3, "bf16", "bf16"),
+                                                 (0.3, "tf32", "bf16"), (0.3, "bf16", "fp16"),
+                                                 (0.3, "bf16", "none")])
 @torch.no_grad()
-def test_patched_layer_forward(device, budget, qk_mode, monkeypatch):
+def test_patched_layer_forward(device, budget, qk_mode, amp, monkeypatch):
     """Two cosine-attention layers (H=4, C=512) through a 13-scale generation
     with the patched forward under bf16 autocast; per layer and step, the
     attention output entering proj against fp32 attention over the oracle's
     q/k/v of the same projection output and the policy's kept keys (scales
     of 1600+ tokens: batch row 1 and heads 0 and 3).  In TF32 dot mode the
     producer writes fp16 q/k, and the oracle attends over q and k rounded to
-    fp16 (TF32's significand)."""
+    fp16 (TF32's significand).  ``amp``: bf16 autocast (the reference's), fp16
+    autocast (fp16 projection and v), or none (an fp32 model: fp32 v)."""
     monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", qk_mode)
     H, B, start_scale = 4, 2, 3
     torch.manual_seed(0)
@@ -308,12 +348,14 @@ def test_patched_layer_forward(device, budget, qk_mode, monkeypatch):
         bs = [1] if big else list(range(B))
         x = torch.randn((B, L, 512), generator=g).to(device)
         for li, layer in enumerate(model):
-            with torch.autocast("cuda", dtype=torch.bfloat16):
+            amp_dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "none": None}[amp]
+            with torch.autocast("cuda", dtype=amp_dtype or torch.bfloat16, enabled=amp_dtype is not None):
                 qkv = torch.nn.functional.linear(
                     x, layer.mat_qkv.weight, bias=torch.cat((layer.q_bias, layer.zero_k_bias, layer.v_bias)))
                 y = layer(x, None, None, SCHED_1M, grid, t)
             torch.cuda.synchronize(device)
-            assert y.dtype == torch.bfloat16 and tuple(y.shape) == (B, L, 512)
+            assert y.dtype == (amp_dtype or torch.float32) and tuple(y.shape) == (B, L, 512)
+            assert qkv.dtype == (amp_dtype or torch.float32)
             arr = qkv.float().cpu().numpy().reshape(B, L, 3, H, D)
             sm = (layer.scale_mul_1H11.reshape(-1).float().clamp_max(layer.max_scale_mul).exp()).cpu().numpy()
             q, k, v = O.produce(arr, scale_mul=sm, table=table, start=P.rope_start(SCHED_1M, t))
