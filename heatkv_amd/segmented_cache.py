@@ -116,6 +116,9 @@ class SegmentedLayerCache:
         # K rows held as split rows (float32-typed; qkv_produce(k_split_rows=True)),
         # fixed by the first step after a reset
         self.k_split_rows = False
+        # the dense prefix kept in place: (K, V) [B, H, rows, D] sized for every
+        # dense scale, each step's rows written by its attention launch
+        self.dense_buf: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
 
     def _ensure_slab(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> None:
         """Slab K/V ``[B, capacity, D]`` (:1092-1144); contents of unowned rows are undefined."""
@@ -179,6 +182,90 @@ class SegmentedLayerCache:
         hit = (plan(old, old_len), plan(cur, cur_len))
         self._dense_current_plans[key] = hit
         return hit
+
+    # ------------------------------------------------------------------ dense prefix in place
+
+    def dense_kv(self) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        """The dense prefix so far, ``[B, H, logical_len, D]`` K and V (a view of
+        the in-place buffer, or the concatenated tensors), or None once the
+        slab holds the cache (or before the first step)."""
+        if self.active:
+            return None
+        if self.dense_buf is not None:
+            return tuple(t[:, :, :self.logical_len] for t in self.dense_buf)
+        if self.cached_k is None:
+            return None
+        return self.cached_k, self.cached_v
+
+    def _dense_capacity(self) -> int:
+        """Rows per head of the dense prefix kept in place: every token of the
+        scales before the first target with removed heads (the slab's
+        activation), or before the final scale when none has any."""
+        act = next((t for t in range(1, self.num_scales) if has_removed(self.removed(t))), self.num_scales - 1)
+        return int(self.schedule.scale_ranges[act - 1][1]) if act >= 1 else 0
+
+    def _in_place_tables(self, heads: int, cap: int, old_len: int, device, batch: int, L: int, qpi: int,
+                         store: bool):
+        """Tables presenting rows ``[0, old_len)`` of each head of the in-place
+        dense prefix ``[B, H, cap, D]`` as a slab ``[B, H*cap, D]``, their work
+        plan, and the append offsets ``h*cap + old_len`` of this step's rows
+        (None when nothing is stored), made once."""
+        key = ("in_place", heads, cap, old_len, str(device), batch, L, qpi, store)
+        hit = self._tables_by_len.get(key)
+        if hit is None:
+            starts = (torch.arange(heads, dtype=torch.int32) * cap).reshape(heads, 1)
+            ends = starts + old_len
+            counts = torch.ones((heads,), dtype=torch.int32)
+            plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
+                                             capacity=heads * cap, device=device, queries_per_item=qpi)
+                    if work_plans_enabled(device) and not _capturing() else None)
+            offs = (starts.reshape(heads) + old_len).to(device) if store else None
+            hit = (starts.to(device), ends.to(device), counts.to(device), plan, offs)
+            self._tables_by_len[key] = hit
+        return hit
+
+    def _in_place_ok(self, q, k, v) -> bool:
+        """Whether this generation's dense prefix can be kept in place: the
+        attention launch must take the append of the step's rows."""
+        return fused_append_enabled() and attention_fuses_append(q.dtype, k.dtype, v.dtype,
+                                                                 k_split_rows=self.k_split_rows)
+
+    def _dense_step_in_place(self, q, k, v, scale_ind: int, scale: float, mode, out_dtype, final: bool):
+        """A dense-prefix step (:1972-2038) on the in-place buffer: attention over
+        the rows so far plus the current scale, whose rows the same launch
+        writes behind them (the reference concatenates them onto the cache);
+        at the first target with removed heads the full buffer is packed into
+        the slab."""
+        B, H, L, D = q.shape
+        old_len = self.logical_len
+        if self.dense_buf is None:
+            cap = self._dense_capacity()
+            self.dense_buf = (torch.empty((B, H, cap, k.shape[3]), dtype=k.dtype, device=k.device),
+                              torch.empty((B, H, cap, v.shape[3]), dtype=v.dtype, device=v.device))
+        buf_k, buf_v = self.dense_buf
+        cap = int(buf_k.shape[2])
+        store = not final
+        if store and old_len + L > cap:
+            raise RuntimeError("dense prefix longer than its in-place buffer")
+        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows)
+        st, en, ct, plan, offs = self._in_place_tables(H, cap, old_len, q.device, B, L, qpi, store)
+        with prof.phase("attention"):
+            out = fused_real_pruning_flat_segmented_attention(
+                q=q, persisted_k=buf_k.reshape(B, H * cap, buf_k.shape[3]),
+                persisted_v=buf_v.reshape(B, H * cap, buf_v.shape[3]), segment_starts=st, segment_ends=en,
+                segment_counts=ct, current_k=k, current_v=v, softmax_scale=scale, softmax_mode=mode,
+                out_dtype=out_dtype, work_plan=plan, append_offsets=offs, k_split_rows=self.k_split_rows)
+        if final:
+            self.reset()
+            return out
+        self.logical_len = old_len + L
+        if has_removed(self.removed(scale_ind + 1)):
+            if self.logical_len != cap:
+                raise RuntimeError("dense prefix packed into the slab before its buffer is full")
+            with prof.phase("compact"):
+                self._activate_from_dense(buf_k, buf_v, scale_ind + 1)
+            self.dense_buf = None
+        return out
 
     # ------------------------------------------------------------------ attention
 
@@ -283,6 +370,8 @@ class SegmentedLayerCache:
 
         if baseline_prefix_enabled() and not self.active and not has_removed(self.removed(scale_ind)):
             # dense prefix (:1972-2038)
+            if self.dense_buf is not None or (old_len == 0 and self._in_place_ok(q, k, v)):
+                return self._dense_step_in_place(q, k, v, scale_ind, softmax_scale, mode, out_dtype, final)
             with prof.phase("attention"):
                 out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
             if final:

@@ -119,7 +119,39 @@ def test_unpruned_policy_stays_dense(cpu_ops):
     for t, (q, k, v) in enumerate(inputs[:-1]):
         cache.step(q, k, v, t, 0.3)
         assert not cache.active
-        assert cache.cached_k.shape[2] == sum(s * s for s in sides[:t + 1])
+        dk, dv = cache.dense_kv()
+        assert dk.shape[2] == sum(s * s for s in sides[:t + 1])
+        # the dense prefix holds every row so far, in order
+        assert torch.equal(dk, torch.cat([inputs[s][1] for s in range(t + 1)], dim=2))
+        assert torch.equal(dv, torch.cat([inputs[s][2] for s in range(t + 1)], dim=2))
+
+
+@pytest.mark.parametrize("fused_append", ["1", "0"])
+def test_dense_prefix_in_place_or_concatenated(cpu_ops, monkeypatch, fused_append):
+    """With the fused append on, the dense prefix lives in one buffer sized
+    for every dense scale (each step's rows written by its attention call);
+    with it off, the cache concatenates as the reference does.  Same outputs
+    and the same packed slab either way."""
+    monkeypatch.setenv("HKV_FUSED_APPEND", fused_append)
+    sides = (1, 2, 4, 6, 8)
+    H, B, D = 3, 2, 16
+    keep = torch.ones((H, len(sides) - 1), dtype=torch.bool)
+    keep[1, 0] = False  # the first removal is at target 4: scales 0-3 are the dense prefix
+    keep[2, 1] = False
+    keep[:, :3] = True
+    keep[0, 3] = False
+    sched = W.schedule_from_keep(keep, sides)
+    cache = sc.SegmentedLayerCache(sched, W.removed_from_keep(keep, len(sides)), num_heads=H)
+    inputs = W.generation_inputs(batch=B, heads=H, sides=sides, seed=9, dtype=torch.float32, head_dim=D)
+    for t, (q, k, v) in enumerate(inputs):
+        out = cache.step(q, k, v, t, D ** -0.5)
+        np.testing.assert_allclose(out.numpy(), _expected(inputs, keep, t, D ** -0.5), rtol=2e-5, atol=2e-5)
+        if t < 3:
+            assert (cache.dense_buf is not None) == (fused_append == "1") and not cache.active
+            if cache.dense_buf is not None:
+                assert cache.dense_buf[0].shape[2] == sum(s * s for s in sides[:4])
+        elif t == 3:
+            assert cache.active and cache.dense_buf is None
 
 
 @pytest.mark.parametrize("layer", [7, 0])
@@ -136,11 +168,12 @@ def test_generation_flow_under_reference_policy(cpu_ops, monkeypatch, fused_appe
     import os
 
     monkeypatch.setenv("HKV_FUSED_APPEND", fused_append)
-    fused_calls = []
+    fused_calls = []   # appends fused into segmented attention calls (heads written)
+    dense_calls = []   # dense-prefix calls that write their rows into the in-place buffer
 
     def counting_attention(**kw):
         if kw.get("append_offsets") is not None:
-            fused_calls.append(int((kw["append_offsets"] >= 0).sum()))
+            (fused_calls if cache.active else dense_calls).append(int((kw["append_offsets"] >= 0).sum()))
         return _cpu_attention(**kw)
 
     monkeypatch.setattr(sc, "fused_real_pruning_flat_segmented_attention", counting_attention)
@@ -178,8 +211,12 @@ def test_generation_flow_under_reference_policy(cpu_ops, monkeypatch, fused_appe
         # layer 7 fuses one head's append at scale 9; layer 0 fuses most heads
         # at scales 8-11 and copies the rest after the attention
         assert sum(fused_calls) > 0 and (layer != 0 or len(fused_calls) == 4), fused_calls
+        # the dense prefix grows in place, every head at every step before the
+        # first target with removed heads
+        act = next(t for t in range(1, len(SIDES_1M)) if any(len(s) for s in removed(t).values()))
+        assert act >= 3 and dense_calls == [H] * act, (act, dense_calls)
     else:
-        assert not fused_calls
+        assert not fused_calls and not dense_calls
 
 
 def test_fused_append_split_under_reference_policy(cpu_ops):
