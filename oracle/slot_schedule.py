@@ -23,10 +23,13 @@ Pinning (tests/test_oracle_schedule.py):
   ``[0, capacity)``, tables sorted by source scale, ``counts[h]`` equal to the
   number of live pairs of head h, and capacity >= the live row count.
 
-Exact offsets of the allocator under *progressive* removal beyond the
-hand-worked cases are otherwise parity unpinned: the reference module imports
-``timm``/``flash_attn`` through ``infinity.models.basic`` and is not importable
-here.
+* under the HeatKV policy's progressive removal (orders/2b.json at budgets
+  0.1 and 0.35, all 32 layers), the product allocator is compared with the
+  reference's own allocator function (tests/golden/slab_2b.json, written by
+  tests/golden/make_slab_golden.py, which compiles and runs just that
+  function from the reference module's text: the module imports ``timm`` /
+  ``flash_attn`` through ``infinity.models.basic`` and cannot be imported
+  here), and this restatement with the product on the same removal sets.
 """
 
 from __future__ import annotations

@@ -10,9 +10,12 @@ and the controller's removed heads for every (target, source, layer).
 
 The allocator run on those removal sets (offsets change as heads are dropped
 between targets) is checked against the allocator restatement in
-oracle/slot_schedule.py and against its invariants; its exact offsets are
-otherwise parity unpinned (the reference's allocator module is not
-importable here).
+oracle/slot_schedule.py, against its invariants, and against the
+reference's own allocator: tests/golden/slab_2b.json, written by
+tests/golden/make_slab_golden.py, holds the capacity and every segment's
+offset and end target of all 32 layers at budgets 0.1 and 0.35 as
+``_segmented_flat_build_static_slot_schedule``
+(enable_real_pruning_fast.py:260-558) gives them.
 """
 
 from __future__ import annotations
@@ -134,6 +137,27 @@ def test_policy_errors_follow_the_reference():
     bad[0][1] = list(bad[0][0])
     with pytest.raises(ValueError, match="duplicate"):
         P.normalize_orders(bad, num_layers=L, num_heads=H, source_scale_start=START)
+
+
+SLAB_GOLD = json.load(open(os.path.join(HERE, "golden", "slab_2b.json")))
+
+
+@pytest.mark.parametrize("budget", sorted(SLAB_GOLD["budgets"]))
+def test_allocator_matches_reference_offsets(budget):
+    """Progressive removal (heads dropped part-way, freed rows reused by best
+    fit): capacity, capacity bound and every (source, head) segment's end
+    target and slab offset of all 32 layers equal the reference allocator's."""
+    ctrl = P.controller_for_budget(float(budget), ORDERS, num_layers=L, num_heads=H, protected_prefix_scales=START)
+    reused = 0
+    for layer, want in enumerate(SLAB_GOLD["budgets"][budget]):
+        got = build_static_slot_schedule(ctrl, layer_idx=layer, num_heads=H)
+        assert (got.capacity, got.capacity_bound) == (want["capacity"], want["capacity_bound"]), layer
+        segs = sorted([g.source_scale, g.head, g.end_target, g.offset] for g in got.segments)
+        assert segs == want["segments"], layer
+        # rows freed by a dropped head are given to a later segment
+        ends = {(s[3], s[2]) for s in want["segments"] if s[2] < 13}
+        reused += any(s[3] == o and s[0] + 1 >= e for s in want["segments"] for o, e in ends)
+    assert reused > 0
 
 
 @pytest.mark.parametrize("budget", [0.1, 0.2])
