@@ -1,6 +1,7 @@
 """Writes tests/golden/slab_2b.json: the reference's static slot schedule
-(slab offsets and capacity) under the HeatKV policy's progressive removal,
-for the parity test of heatkv_amd/slab_schedule.py.
+(slab offsets and capacity, and digests of its offset tables and copy
+descriptors) under the HeatKV policy's progressive removal, for the parity
+test of heatkv_amd/slab_schedule.py.
 
 Run in the build container only (it reads the reference from
 /root/reference; nothing here runs on the GPU host):
@@ -25,11 +26,13 @@ token ranges), on the reference's orders/2b.json (orders_2b.json here).
 from __future__ import annotations
 
 import ast
+import hashlib
 import json
 import os
 import sys
 import typing
 
+import numpy as np
 import torch
 
 REF = "/root/reference"
@@ -47,6 +50,22 @@ class _Layer:
 
     def __init__(self, num_heads):
         self.num_heads = num_heads
+
+
+def digest(*arrays) -> str:
+    """First 16 hex digits of the SHA-256 of the arrays' shapes and int64 values."""
+    h = hashlib.sha256()
+    for a in arrays:
+        a = np.asarray(a, dtype=np.int64)
+        h.update(np.asarray(a.shape, dtype=np.int64).tobytes())
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()[:16]
+
+
+def runs_digest(runs, sequence_len) -> str:
+    """Digest of a copy-run list flattened to (dst_start, src_start, length) items in order."""
+    items = [(it["dst_start"], it["src_start"], it["length"]) for r in runs for it in r["copy_items"]]
+    return digest(np.asarray(items, dtype=np.int64).reshape(-1, 3), [sequence_len])
 
 
 def reference_allocator():
@@ -89,8 +108,18 @@ def main():
             # one row per (source scale, head) segment: source, head, end target, offset
             segs = sorted((int(s["source_scale"]), int(s["head"]), int(s["end_target"]), int(s["offset"]))
                           for s in res["segments"])
+            # per-target offset tables (starts, ends, counts) and copy runs
+            # (activation from the dense prefix of each target, append of
+            # each scale for the next), as digests of their exact values
+            tables = {str(t): digest(*(x.numpy() for x in res["metadata_cpu_by_target"][t]))
+                      for t in sorted(res["metadata_cpu_by_target"])}
+            activation = {str(t): runs_digest(runs, res["old_pack_cache_lens_by_target"][t])
+                          for t, runs in sorted(res["old_pack_runs_by_target"].items())}
+            append = {str(s): runs_digest(runs, runs[0]["sequence_len"] if runs else 0)
+                      for (s, _), runs in sorted(res["append_runs_by_key"].items())}
             per_layer.append({"capacity": int(res["capacity"]), "capacity_bound": int(res["capacity_bound"]),
-                              "segments": [list(s) for s in segs]})
+                              "segments": [list(s) for s in segs], "tables": tables, "activation": activation,
+                              "append": append})
         out["budgets"][str(budget)] = per_layer
     with open(os.path.join(HERE, "slab_2b.json"), "w") as fh:
         json.dump(out, fh, separators=(",", ":"), sort_keys=True)

@@ -13,13 +13,15 @@ between targets) is checked against the allocator restatement in
 oracle/slot_schedule.py, against its invariants, and against the
 reference's own allocator: tests/golden/slab_2b.json, written by
 tests/golden/make_slab_golden.py, holds the capacity and every segment's
-offset and end target of all 32 layers at budgets 0.1 and 0.35 as
+offset and end target of all 32 layers at budgets 0.1 and 0.35, and
+digests of their offset tables and copy descriptors, as
 ``_segmented_flat_build_static_slot_schedule``
 (enable_real_pruning_fast.py:260-558) gives them.
 """
 
 from __future__ import annotations
 
+import hashlib
 import json
 import os
 
@@ -142,11 +144,28 @@ def test_policy_errors_follow_the_reference():
 SLAB_GOLD = json.load(open(os.path.join(HERE, "golden", "slab_2b.json")))
 
 
+def _digest(*arrays) -> str:
+    """SHA-256 (16 hex digits) of the arrays' shapes and int64 values, as the golden file's."""
+    h = hashlib.sha256()
+    for a in arrays:
+        a = np.asarray(a, dtype=np.int64)
+        h.update(np.asarray(a.shape, dtype=np.int64).tobytes())
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()[:16]
+
+
+def _plan_digest(plan) -> str:
+    items = np.asarray(list(zip(plan.dst_starts, plan.src_starts, plan.lengths)), dtype=np.int64).reshape(-1, 3)
+    return _digest(items, [plan.sequence_len if plan.lengths else 0])
+
+
 @pytest.mark.parametrize("budget", sorted(SLAB_GOLD["budgets"]))
 def test_allocator_matches_reference_offsets(budget):
     """Progressive removal (heads dropped part-way, freed rows reused by best
     fit): capacity, capacity bound and every (source, head) segment's end
-    target and slab offset of all 32 layers equal the reference allocator's."""
+    target and slab offset of all 32 layers equal the reference allocator's,
+    and so do the offset tables of every target and the copy descriptors of
+    every activation and append (compared through digests of their values)."""
     ctrl = P.controller_for_budget(float(budget), ORDERS, num_layers=L, num_heads=H, protected_prefix_scales=START)
     reused = 0
     for layer, want in enumerate(SLAB_GOLD["budgets"][budget]):
@@ -154,6 +173,9 @@ def test_allocator_matches_reference_offsets(budget):
         assert (got.capacity, got.capacity_bound) == (want["capacity"], want["capacity_bound"]), layer
         segs = sorted([g.source_scale, g.head, g.end_target, g.offset] for g in got.segments)
         assert segs == want["segments"], layer
+        assert {str(t): _digest(*(x.numpy() for x in tab)) for t, tab in got.tables.items()} == want["tables"]
+        assert {str(t): _plan_digest(p) for t, p in got.activation_plans.items()} == want["activation"], layer
+        assert {str(s): _plan_digest(p) for (s, _), p in got.append_plans.items()} == want["append"], layer
         # rows freed by a dropped head are given to a later segment
         ends = {(s[3], s[2]) for s in want["segments"] if s[2] < 13}
         reused += any(s[3] == o and s[0] + 1 >= e for s in want["segments"] for o, e in ends)
