@@ -57,6 +57,8 @@ prints one JSON line.
   ``attention_frac_of_gemm`` relates the attention to the former.
 * ``skewed_ragged``: the skewed-ragged final step (B=16, H=16, seed 3,
   retained lengths log-uniform in [0, 6425]) as its own leg.
+* The secondary legs' ms per step (``real_model``, ``budgets_8b_class``,
+  ``skewed_ragged``) is the median of three back-to-back timing windows.
 * ``cpu_baseline``: the reference CPU path restated in torch (gather +
   scaled_dot_product_attention, fp32) on the host cores over whole steps
   (median of 5 after a warm-up), rank 0 only; ``cores`` = the threads used
@@ -179,6 +181,17 @@ def time_attention(kw, device, steps, warmup):
     host_us = (time.perf_counter() - host0) / steps * 1e6
     torch.cuda.synchronize(device)
     return t0.elapsed_time(t1) / steps, host_us
+
+
+def time_attention_median(kw, device, steps, warmup, windows=3):
+    """Median over ``windows`` back-to-back timing windows of ``steps`` calls
+    each (one warm-up of ``warmup`` calls first): the secondary legs report
+    the median, so one window stretched by a host-side stall (the host
+    descheduled while the GPU queue drains) does not stand for the kernel."""
+    ms = []
+    for i in range(windows):
+        ms.append(time_attention(kw, device, steps, warmup if i == 0 else 0)[0])
+    return sorted(ms)[len(ms) // 2]
 
 
 def time_pack(wl, device, reps=20):
@@ -437,7 +450,7 @@ def time_real_model(device, steps=50, warmup=20):
     kw["work_plan"] = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len, queries_per_item=qpi)
                        if work_plans_enabled(device) else None)
     # fp32 K split on every call (the operator's own split, two extra launches)
-    ms_split, _ = time_attention(kw, device, steps, warmup)
+    ms_split = time_attention_median(kw, device, steps, warmup)
     # K as split rows, the form the producer writes and the cache keeps
     # (qkv_produce(k_split_rows=True)): the model path
     from heatkv_amd.real_pruning_fused_attention import _split_rows
@@ -447,13 +460,13 @@ def time_real_model(device, steps=50, warmup=20):
     for name, t in fp32_k.items():
         kw[name] = _split_rows(t, stream).view(torch.float32)
     kw["k_split_rows"] = True
-    ms, _ = time_attention(kw, device, steps, warmup)
+    ms = time_attention_median(kw, device, steps, warmup)
     del kw["k_split_rows"]
     kw.update(fp32_k)
     for name in ("q", "current_k", "persisted_k"):
         kw[name] = kw[name].half()
     kw["work_plan"] = plan16
-    ms16, _ = time_attention(kw, device, steps, warmup)
+    ms16 = time_attention_median(kw, device, steps, warmup)
     flops = wl.attention_flops()
     kernel = f"split-row kernel ({qpi}-query items), K held as split rows as the producer writes it"
     return {"what": f"2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 ({kernel})",
@@ -523,7 +536,7 @@ def time_final_step(config, device, steps=20, warmup=10):
 
     wl = W.config(config)
     kw = attention_call(wl, device)
-    ms, _ = time_attention(kw, device, steps, warmup)
+    ms = time_attention_median(kw, device, steps, warmup)
     flops = wl.attention_flops()
     rows = wl.retained_rows()
     del kw
@@ -546,7 +559,7 @@ def time_budgets(device, steps=20, warmup=10):
     for budget in (0.05, 0.1, 0.2, 1.0):
         wl = W.with_budget(base, budget)
         kw = attention_call(wl, device)
-        ms, _ = time_attention(kw, device, steps, warmup)
+        ms = time_attention_median(kw, device, steps, warmup)
         flops = wl.attention_flops()
         out[str(budget)] = {"ms_per_step": round(ms, 4), "flops_per_step": flops,
                             "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
