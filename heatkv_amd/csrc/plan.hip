@@ -8,7 +8,9 @@
 // call (as the reference uploads its offset tables once per layer and target,
 // enable_real_pruning_fast.py:592-608).  A plan is a list of units, one per
 // workgroup in dispatch order: a whole item (b, h, query tile of the
-// kernel's bm queries) or one of the two key-range parts of a cut item.
+// kernel's bm queries) or one of the two key-range parts of a cut item,
+// and whether the 16-bit kernel shares a CU's SIMDs tile by tile (items of
+// unequal length).
 //
 // Choosing the cuts.  The hardware dispatches workgroups in id order to
 // whatever slot frees first, i.e. list scheduling.  The plan simulates it
@@ -207,6 +209,17 @@ int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
     for (int32_t j = 0; j < per_h; ++j) items.push_back({h, j, n});
   }
   const int32_t N = static_cast<int32_t>(items.size());
+  // Items of unequal length (more than 5/4 between the longest and the
+  // shortest): the kernel shares a CU's SIMDs between its two workgroups
+  // tile by tile (wave priority), so the items progress at the rates the
+  // dispatch simulation assumes.  Equal items (every head keeping as many
+  // rows) balance without it and run faster when the workgroups drift apart.
+  int32_t n_min = 0, n_max = 0;
+  for (const Item& it : items) {
+    n_min = n_min == 0 || it.n < n_min ? it.n : n_min;
+    n_max = it.n > n_max ? it.n : n_max;
+  }
+  const int32_t shared = 4LL * n_max > 5LL * n_min ? 1 : 0;
 
   // units in dispatch order, one list per XCD (a single list when not dealt)
   struct Unit {
@@ -291,7 +304,7 @@ int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
       o[4] = x->cut;
       o[5] = x->part;
     }
-    o[6] = 0;
+    o[6] = x == nullptr ? 0 : shared;
     o[7] = 0;
   };
   if (lists.size() == 1) {

@@ -124,12 +124,14 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const bool planned = a.plan != nullptr;
   int32_t p0 = 0, p1 = 0;
   bool cut = false;
+  bool shared = false;  // alternate the wave priority by tile (the plan says so)
   if (planned) {
     // the unit of this workgroup from the caller's work plan
     const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
     const int32_t ph = pu[0], pj = pu[1], pcut = pu[4], ppart = pu[5];
     p0 = pu[2];
     p1 = pu[3];
+    shared = pu[6] != 0;
     if (ph < 0 || ph >= H || pj < 0 || pj >= a.batch * n_qt) return;  // not a unit of this launch
     w.h = ph;
     w.b = pj / n_qt;
@@ -321,13 +323,17 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   auto step = [&](f32x16_t (&scur)[2], f32x16_t (&snext)[2], int t) {
     // The two workgroups of a CU share its SIMDs, whose issue favours the
     // older waves, so one item ran at a fraction of the other's rate until
-    // it finished.  Alternating the priority by tile (with the workgroup id
-    // in the parity) shares the SIMDs tile by tile: -1.9 % on the 2B final
-    // step, -1 to -3 % on the sweep's last scales.
-    if (((t + static_cast<int>(blockIdx.x)) & 1) == 0)
-      __builtin_amdgcn_s_setprio(1);
-    else
-      __builtin_amdgcn_s_setprio(0);
+    // it finished.  With items of unequal length (as the plan marks them)
+    // the priority alternates by tile, with the workgroup id in the parity,
+    // so the SIMDs are shared tile by tile and the items progress as the
+    // plan assumes: -1.9 % on the 2B final step, -1 to -3 % on the sweep's
+    // last scales; equal items (+3 % with it) keep the hardware's order.
+    if (shared) {
+      if (((t + static_cast<int>(blockIdx.x)) & 1) == 0)
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(0);
+    }
     wait_vmcnt<0>();  // this wave's K(t + 1) or V(t)
     __syncthreads();
     if (k_wave) {

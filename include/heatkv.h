@@ -205,7 +205,10 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
  * to the 8 XCDs (workgroup id % 8) in chunks of a (batch row, head)'s query
  * tiles, each XCD's list padded to equal length with empty units (head -1,
  * the workgroup leaves at once).  Unit: head, batch row * n_qt + query tile,
- * first and end key tile, cut index (-1 = whole item), part (0 or 1), 0, 0.
+ * first and end key tile, cut index (-1 = whole item), part (0 or 1), a flag
+ * (1 when the items' key tile counts differ by more than 5/4: the 16-bit
+ * kernel then alternates its wave priority by tile so the two workgroups of a
+ * CU share its SIMDs evenly; 0 otherwise and in empty units), 0.
  * Host-only: no device call.  No counterpart in the reference (its tables
  * are the whole plan: the Triton grid walks them).
  */
