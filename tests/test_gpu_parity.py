@@ -107,6 +107,33 @@ def test_attention_config2_heads(device):
     _check_workload(wl, device, heads=heads, batches=[1])
 
 
+def test_attention_priority_flag_is_schedule_only(device):
+    """The work plan's field 6 (set when the items differ in length: the
+    16-bit kernel then alternates its wave priority by tile) changes only the
+    order in which each SIMD issues its two workgroups' instructions: the 2B
+    final step gives the same bits with the field set and cleared."""
+    print("[attn] config 2, plan priority field set vs cleared", flush=True)
+    wl = W.config(2)
+    slab_k, slab_v = W.build_slab(wl, device)
+    st, en, ct = wl.schedule.device_tables(wl.target, device)
+    plan = wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len)
+    assert bool((plan[plan[:, 0] >= 0, 6] == 1).all())
+    cleared = plan.clone()
+    cleared[:, 6] = 0
+    cleared.hkv_queries_per_item = plan.hkv_queries_per_item
+    q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
+    res = []
+    for p in (plan, cleared):
+        out, lse = fused_real_pruning_flat_segmented_attention(
+            q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
+            segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale,
+            return_lse=True, work_plan=p)
+        torch.cuda.synchronize(device)
+        res.append((out, lse))
+    assert np.array_equal(bits(res[0][0]), bits(res[1][0]))
+    assert np.array_equal(bits(res[0][1]), bits(res[1][1]))
+
+
 def test_attention_config5_heads(device):
     wl = W.config(5)
     r = wl.retained_rows()
