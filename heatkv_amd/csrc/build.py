@@ -33,6 +33,13 @@ FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
+# Per-source flags.  The 16-bit attention kernel takes its work plan's
+# pointer and unit count as its first two arguments, preloaded into SGPRs at
+# wave launch, so the unit's load needs no kernel-argument load first.
+EXTRA = {
+    "seg_attn_direct.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
+}
+
 
 def _hipcc():
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -58,7 +65,7 @@ def build(verbose: bool = False) -> str:
     for src in SOURCES:
         obj = os.path.join(out_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj])
+        cmds.append([hipcc, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(HERE, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         for msg in ex.map(_run, cmds):
             if verbose and msg.strip():
