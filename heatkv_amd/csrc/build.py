@@ -33,11 +33,13 @@ FLAGS = [
     f"-I{os.path.join(ROOT, 'include')}",
 ]
 
-# Per-source flags.  The 16-bit attention kernel takes its work plan's
-# pointer and unit count as its first two arguments, preloaded into SGPRs at
-# wave launch, so the unit's load needs no kernel-argument load first.
+# Per-source flags.  The 16-bit and split-row attention kernels take their
+# work plan's pointer and unit count as their first two arguments, preloaded
+# into SGPRs at wave launch, so the unit's load needs no kernel-argument load
+# first.
 EXTRA = {
     "seg_attn_direct.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
+    "seg_attn_split.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
 }
 
 

@@ -139,7 +139,9 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
 }
 
 template <int VDT>
-__global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const AttnArgs a, const Scalars sc,
+__global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const int32_t* __restrict__ plan_p,
+                                                                     const int32_t n_units, const AttnArgs a,
+                                                                     const Scalars sc,
                                                                      const int32_t n_qt) {
   constexpr int kThreads = kSThreads;
   constexpr int kBM = kSBM;
@@ -158,6 +160,16 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform by construction
   const int g = lane >> 5;
+  // This workgroup's plan unit, loaded with the kernel arguments: the plan
+  // pointer and unit count are preloaded into SGPRs (as in the 16-bit
+  // kernel).
+  int32_t pu[kPlanInts] = {};
+  const bool planned = plan_p != nullptr && static_cast<int32_t>(blockIdx.x) < n_units;
+  if (planned) {
+    const int32_t* src = plan_p + static_cast<int64_t>(blockIdx.x) * kPlanInts;
+#pragma unroll
+    for (int i = 0; i < kPlanInts; ++i) pu[i] = src[i];
+  }
 
   // The unit: from the caller's work plan (a whole item or one key-range
   // part of a cut item, merged through the workspace), else the workgroup's
@@ -165,8 +177,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const Attn
   WorkItem w;
   Unit un{0, 0, 1, 0, 0};
   int32_t p0 = 0, p1 = 0;
-  if (a.plan != nullptr) {
-    const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
+  if (planned) {
     const int32_t ph = pu[0], pj = pu[1], pcut = pu[4], ppart = pu[5];
     p0 = pu[2];
     p1 = pu[3];
@@ -444,7 +455,8 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   }
   const int64_t grid = a.plan != nullptr ? a.plan_units : items;
   if (grid <= 0) return hipSuccess;
-  seg_attn_split_kernel<VDT><<<dim3(static_cast<uint32_t>(grid)), kSThreads, 0, st>>>(b, s, n_qt);
+  seg_attn_split_kernel<VDT><<<dim3(static_cast<uint32_t>(grid)), kSThreads, 0, st>>>(
+      b.plan, b.plan != nullptr ? static_cast<int32_t>(grid) : 0, b, s, n_qt);
   return hipGetLastError();
 }
 
