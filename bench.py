@@ -71,6 +71,7 @@ prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -173,12 +174,20 @@ def time_attention(kw, device, steps, warmup):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(device)
-    host0 = time.perf_counter()
-    t0.record(stream)
-    for _ in range(steps):
-        attn(**kw)
-    t1.record(stream)
-    host_us = (time.perf_counter() - host0) / steps * 1e6
+    # no garbage-collector pause while the host enqueues the timed steps (a
+    # pause then would leave the GPU idle inside the timed region)
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        host0 = time.perf_counter()
+        t0.record(stream)
+        for _ in range(steps):
+            attn(**kw)
+        t1.record(stream)
+        host_us = (time.perf_counter() - host0) / steps * 1e6
+    finally:
+        if gc_was_on:
+            gc.enable()
     torch.cuda.synchronize(device)
     return t0.elapsed_time(t1) / steps, host_us
 
