@@ -23,6 +23,10 @@ HKV_ERR_UNSUPPORTED = -2
 HKV_ERR_LAUNCH = -3
 HKV_ERR_DEVICE = -4
 
+# HKV_VERSION of include/heatkv.h these bindings follow (SIGNATURES below);
+# load() refuses a library built from another version of the header.
+ABI_VERSION = (0 << 16) | (2 << 8) | 0
+
 DTYPE_CODES = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
 DTYPE_SPLIT_ROWS = 4  # K only: fp32 rows as bf16 high parts then low parts (hkv_split_rows)
 
@@ -102,6 +106,12 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        have = int(lib.hkv_version())
+        if have != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} reports ABI version {have >> 16}.{(have >> 8) & 255}.{have & 255}; these "
+                f"bindings need {ABI_VERSION >> 16}.{(ABI_VERSION >> 8) & 255}.{ABI_VERSION & 255} -- rebuild it "
+                "with `python heatkv_amd/csrc/build.py`")
         _lib = lib
     return _lib
 

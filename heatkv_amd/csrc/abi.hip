@@ -79,7 +79,9 @@ void* device_scratch(int device, hipStream_t stream) {
 
 extern "C" {
 
-int32_t hkv_version(void) { return (0 << 16) | (1 << 8) | 0; }
+// 0.2.0: hkv_segmented_attention's dot modes and work plan arguments, the
+// split-row K dtype; a work plan with no units is refused.
+int32_t hkv_version(void) { return HKV_VERSION; }
 
 int32_t hkv_device_ok(int32_t device) {
   int n = 0;
@@ -192,8 +194,10 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
     return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
   if (value_dot_mode != 0 && value_dot_mode != 2)
     return fail(HKV_ERR_INVALID_ARG, "value_dot_mode must be 0 (bf16) or 2 (fp32) (got %d)", value_dot_mode);
-  if (work_plan != nullptr && plan_units < 0)
-    return fail(HKV_ERR_INVALID_ARG, "plan_units must be >= 0 (got %d)", plan_units);
+  // every (batch, head, query tile) item has a unit in a plan built for the
+  // call, so a plan without units cannot match it (its outputs would stay unwritten)
+  if (work_plan != nullptr && plan_units <= 0)
+    return fail(HKV_ERR_INVALID_ARG, "plan_units must be > 0 with a work plan (got %d)", plan_units);
   if (head_dim != 128)
     return fail(HKV_ERR_UNSUPPORTED, "real_scale_fused_segmented v1 only supports head_dim=128");
   if (cur_len <= 0)

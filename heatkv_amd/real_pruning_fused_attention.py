@@ -85,8 +85,10 @@ def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, ba
     an int32 tensor ``[units, 8]`` on ``device`` (host when None) to pass as
     ``work_plan`` with every call on those tables.  ``queries_per_item`` is
     the kernel's (:func:`attention_queries_per_item`: 128, or 256 for fp32
-    q/k with 16-bit v); the tensor carries it as ``hkv_queries_per_item`` and
-    the operator checks it.  Built on the host by
+    q/k with 16-bit v); the tensor carries it as ``hkv_queries_per_item``
+    and the batch size and length as ``hkv_plan_shape``, and the operator
+    checks both (a copy made with ``clone()`` / ``to()`` loses them and is
+    refused).  Built on the host by
     ``hkv_segmented_attention_plan``; ``slots`` defaults to the device's
     resident attention workgroups for that kernel.  No counterpart in the
     reference, whose Triton grid walks the tables directly."""
@@ -123,6 +125,7 @@ def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, ba
     if device is not None:
         out = out.to(device)
     out.hkv_queries_per_item = int(queries_per_item)
+    out.hkv_plan_shape = (int(batch_size), int(current_len))
     return out
 
 
@@ -294,6 +297,27 @@ def pack_flat_segments_kv(
     return dst_k, dst_v
 
 
+def _promote_mixed_qk(q, persisted_k, current_k, qk_mode: int, append_offsets):
+    """q and k of different dtypes: the reference's fp32-class QK modes cast
+    both to fp32 before the product (real_pruning_fused_attention.py:143-153),
+    so here the 16-bit side is widened to fp32 (exactly) and the call runs the
+    fp32 q/k kernels.  The default mode's dot takes one operand type, so the
+    reference's Triton compile fails there; this raises instead."""
+    if qk_mode == 0:
+        raise RuntimeError(
+            "real_scale_fused_segmented requires q and k of one dtype under "
+            "REAL_PRUNING_FUSED_QK_DOT_MODE=bf16; tf32 or fp32 take q and k of different dtypes")
+    if q.dtype != torch.float32:
+        q = q.float()
+    if current_k.dtype != torch.float32:
+        if append_offsets is not None:
+            raise ValueError("append_offsets: k is widened to fp32 for an fp32 q, so the call cannot "
+                             "append into the 16-bit slab; append after the call")
+        current_k = current_k.float()
+        persisted_k = persisted_k.float()
+    return q, persisted_k, current_k
+
+
 def fused_real_pruning_flat_segmented_attention(
     *,
     q: torch.Tensor,
@@ -392,8 +416,6 @@ def fused_real_pruning_flat_segmented_attention(
             raise RuntimeError(
                 f"real_scale_fused_segmented supports only float16, bfloat16, or float32 {what} tensors"
             )
-    if q.dtype != current_k.dtype:
-        raise RuntimeError("real_scale_fused_segmented requires q and k of one dtype")
     if out_dtype is None:
         out_dtype = q.dtype
     if out_dtype not in (torch.float16, torch.bfloat16, torch.float32):
@@ -405,6 +427,8 @@ def fused_real_pruning_flat_segmented_attention(
         _positive_int_env(knob, default)
     qk_mode = _fused_qk_dot_mode_id()
     value_mode = _fused_value_dot_mode_id()
+    if q.dtype != current_k.dtype and not k_split_rows:
+        q, persisted_k, current_k = _promote_mixed_qk(q, persisted_k, current_k, qk_mode, append_offsets)
 
     _lib.require_device(q.device)
     if append_offsets is not None and not (persisted_k.is_contiguous() and persisted_v.is_contiguous()):
@@ -434,7 +458,14 @@ def fused_real_pruning_flat_segmented_attention(
         if work_plan.device != q.device:
             raise ValueError("work_plan must be on the same device as q")
         want = attention_queries_per_item(q.dtype, current_k.dtype, current_v.dtype, k_split_rows=k_split_rows)
-        have = getattr(work_plan, "hkv_queries_per_item", want)
+        have = getattr(work_plan, "hkv_queries_per_item", None)
+        shape = getattr(work_plan, "hkv_plan_shape", None)
+        if have is None or shape is None:
+            raise ValueError("work_plan must be a tensor made by segmented_attention_plan (it records the item "
+                             "size, batch size and length it was built for; clone() / to() drop that record)")
+        if tuple(shape) != (batch_size, current_len):
+            raise ValueError(f"work_plan was built for batch {shape[0]} and length {shape[1]}; this call has "
+                             f"batch {batch_size} and length {current_len}")
         if have != want:
             raise ValueError(f"work_plan was built for {have}-query items; this call's kernel takes {want} "
                              "(segmented_attention_plan(..., queries_per_item=attention_queries_per_item(...)))")

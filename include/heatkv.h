@@ -47,7 +47,10 @@ int32_t hkv_concat_kv(const void* old_k, const void* new_k, const void* old_v, c
                       void* out_v, int64_t groups, int64_t t_old, int64_t t_new, int64_t k_row_bytes,
                       int64_t v_row_bytes, void* stream);
 
-/* Library version, (major << 16) | (minor << 8) | patch. Loader check. */
+/* Library version, (major << 16) | (minor << 8) | patch: HKV_VERSION of the
+ * header the library was built with.  A loader compares it with the version
+ * of the header (or bindings) it was written against and refuses a mismatch. */
+#define HKV_VERSION ((0 << 16) | (2 << 8) | 0)
 int32_t hkv_version(void);
 
 /* 1 when `device` is a gfx950 GPU this build can run on, else 0.

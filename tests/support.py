@@ -90,3 +90,34 @@ class SelfAttention(torch.nn.Module):
 
     def forward(self, *args, **kwargs):  # pragma: no cover - replaced when enabled
         raise NotImplementedError("unpatched test layer")
+
+
+def kept_keys_reference(inputs, kept_scales, t: int, scale: float, *, workers: int = 16):
+    """fp32 oracle attention of generation step ``t`` over exactly the keys a
+    policy keeps: head h attends to the rows of the prior scales
+    ``kept_scales(h)`` (in that order), then to its own current rows.
+    ``inputs[s]`` = ``(q, k, v)`` ``[B, H, n_s, D]`` of scale s.  Every (b, h)
+    is computed (the oracle's thread pool over the pairs); returns
+    ``(out [B, L, H*D], lse [B, H, L])``."""
+    from oracle import segmented_attention as oattn
+
+    q, k, v = inputs[t]
+    B, H, _, D = q.shape
+    pieces_k, pieces_v, starts, ends = [], [], [], []
+    off = 0
+    for h in range(H):
+        n = 0
+        for s in kept_scales(h):
+            pieces_k.append(inputs[s][1][:, h])
+            pieces_v.append(inputs[s][2][:, h])
+            n += int(inputs[s][1].shape[2])
+        starts.append(off)
+        ends.append(off + n)
+        off += n
+    slab_k = torch.cat(pieces_k, dim=1) if pieces_k else torch.zeros((B, 0, D), dtype=k.dtype)
+    slab_v = torch.cat(pieces_v, dim=1) if pieces_v else torch.zeros((B, 0, D), dtype=v.dtype)
+    st = np.asarray(starts, np.int32).reshape(H, 1)
+    en = np.asarray(ends, np.int32).reshape(H, 1)
+    ct = np.ones(H, np.int32)
+    return oattn.flat_segmented_attention(to_np(q), to_np(slab_k), to_np(slab_v), st, en, ct, to_np(k), to_np(v),
+                                          scale, workers=workers)

@@ -117,3 +117,24 @@ def test_qkv_produce_rejects_cpu_and_non_bf16():
 
     with pytest.raises(RuntimeError, match="GPU only"):
         qkv_produce(torch.zeros((1, 4, 3 * 2 * 128), dtype=torch.bfloat16), 2)
+
+
+def test_mixed_qk_promotion_rules():
+    """q and k of different dtypes: refused in the default QK mode, the 16-bit
+    side widened to fp32 (exactly) in the fp32-class modes, and a widened k
+    refuses the in-launch append (it would write a copy)."""
+    from heatkv_amd.real_pruning_fused_attention import _promote_mixed_qk
+
+    q = torch.randn(1, 2, 8, 128)
+    k = torch.randn(1, 2, 8, 128).to(torch.bfloat16)
+    sk = torch.randn(1, 16, 128).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="one dtype"):
+        _promote_mixed_qk(q, sk, k, 0, None)
+    q2, sk2, k2 = _promote_mixed_qk(q, sk, k, 1, None)
+    assert q2 is q and sk2.dtype == torch.float32 and k2.dtype == torch.float32
+    assert torch.equal(k2, k.float()) and torch.equal(sk2, sk.float())
+    with pytest.raises(ValueError, match="append after the call"):
+        _promote_mixed_qk(q, sk, k, 2, torch.zeros(2, dtype=torch.int32))
+    qb = q.to(torch.bfloat16)
+    q3, sk3, k3 = _promote_mixed_qk(qb, sk.float(), k.float(), 2, torch.zeros(2, dtype=torch.int32))
+    assert q3.dtype == torch.float32 and torch.equal(q3, qb.float()) and k3.dtype == torch.float32

@@ -112,3 +112,49 @@ def test_all_fp32_modes_together(device, monkeypatch):
     out_err, lse_err = _errors(case, 1.0, device, monkeypatch, qk_mode="ieee", value_mode="fp32")
     print(f"[dot] out max-abs {out_err:.3e} lse max-abs {lse_err:.3e}", flush=True)
     assert out_err <= 1e-4 and lse_err <= 5e-5
+
+
+@pytest.mark.parametrize("mode", ["tf32", "fp32"])
+@pytest.mark.parametrize("qdt,kdt", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float16, torch.bfloat16)])
+def test_mixed_qk_dtypes(qdt, kdt, mode, device, monkeypatch):
+    """q and k of different dtypes under the fp32-class QK modes, as the
+    reference casts both to fp32 there (real_pruning_fused_attention.py:
+    143-153): cosine-attention scores of +-100 against the fp64 oracle on the
+    same (rounded) values; the fp32 mode's 3 pieces keep the LSE within 5e-5,
+    the tf32 mode's 2 pieces within the contract.  The output keeps q's dtype."""
+    print(f"[dot] mixed q {qdt} / k {kdt}, QK {mode}", flush=True)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", mode)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_VALUE_DOT_MODE", "bf16")
+    q, sk, sv, (st, en, ct), ck, cv = _case(85, torch.float32, torch.bfloat16, cosine=True)
+    q, sk, ck = q.to(qdt), sk.to(kdt), ck.to(kdt)
+    out, lse = fused_real_pruning_flat_segmented_attention(
+        q=q.to(device), persisted_k=sk.to(device), persisted_v=sv.to(device), segment_starts=st.to(device),
+        segment_ends=en.to(device), segment_counts=ct.to(device), current_k=ck.to(device),
+        current_v=cv.to(device), softmax_scale=1.0, return_lse=True)
+    torch.cuda.synchronize(device)
+    assert out.dtype == qdt
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q).astype(np.float64), to_np(sk).astype(np.float64), to_np(sv).astype(np.float64),
+        st.numpy(), en.numpy(), ct.numpy(), to_np(ck).astype(np.float64), to_np(cv).astype(np.float64),
+        1.0, dtype=np.float64)
+    o = out.double().cpu().numpy()
+    l = lse.double().cpu().numpy()
+    assert np.isfinite(o).all() and np.isfinite(l).all()
+    oerr = np.abs(o - ref_out)
+    lerr = float(np.abs(l - ref_lse).max())
+    print(f"[dot] out max-abs {oerr.max():.3e} mean-abs {oerr.mean():.3e} lse max-abs {lerr:.3e}", flush=True)
+    assert oerr.max() <= 2e-2 and oerr.mean() <= 2e-3
+    assert lerr <= (5e-5 if mode == "fp32" else 1e-3)
+
+
+def test_mixed_qk_dtypes_default_mode_raises(device, monkeypatch):
+    """The default (bf16) QK mode takes one operand type, as the reference's
+    Triton dot does."""
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16")
+    q, sk, sv, (st, en, ct), ck, cv = _case(86, torch.bfloat16, torch.bfloat16, L=64, cap=200, S=2)
+    with pytest.raises(RuntimeError, match="one dtype"):
+        fused_real_pruning_flat_segmented_attention(
+            q=q.float().to(device), persisted_k=sk.to(device), persisted_v=sv.to(device),
+            segment_starts=st.to(device), segment_ends=en.to(device), segment_counts=ct.to(device),
+            current_k=ck.to(device), current_v=cv.to(device), softmax_scale=0.125)

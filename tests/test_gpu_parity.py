@@ -121,6 +121,7 @@ def test_attention_priority_flag_is_schedule_only(device):
     cleared = plan.clone()
     cleared[:, 6] = 0
     cleared.hkv_queries_per_item = plan.hkv_queries_per_item
+    cleared.hkv_plan_shape = plan.hkv_plan_shape
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
     res = []
     for p in (plan, cleared):

@@ -5,8 +5,8 @@ freed by a dropped (source scale, head) are reused by later appends.
 
 Per step, the attention output of SegmentedLayerCache (HIP pack + attention)
 against fp32 attention over exactly the keys the policy keeps for each head
-(oracle/segmented_attention.py), and after each append the live slab rows
-bit-exact against the source K/V.  The removed sets come from
+(oracle/segmented_attention.py), every (batch row, head) at every scale, and
+after each append the live slab rows bit-exact against the source K/V.  The removed sets come from
 heatkv_amd/policy.py, pinned to the reference by tests/test_policy.py.
 """
 
@@ -24,8 +24,7 @@ from heatkv_amd import policy as P
 from heatkv_amd import segmented_cache as sc
 from heatkv_amd import workloads as W
 from heatkv_amd.slab_schedule import SIDES_1M, build_static_slot_schedule
-from oracle import segmented_attention as oattn
-from support import assert_attention_close, bits, to_np
+from support import assert_attention_close, bits, kept_keys_reference, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -36,22 +35,6 @@ L_MODEL, H, START = 32, 16, 3
 def _kept_sources(ctrl, layer, t, h):
     removed = ctrl.removed_heads_by_source_for(layer, t)
     return [s for s in range(t) if h not in removed.get(s, set())]
-
-
-def _reference(inputs, ctrl, layer, t, scale, heads, batches):
-    q, k, v = inputs[t]
-    B, Hq, L, D = q.shape
-    out = np.full((B, L, Hq * D), np.nan, np.float32)
-    for h in heads:
-        srcs = _kept_sources(ctrl, layer, t, h)
-        kk = torch.cat([inputs[s][1][:, h] for s in srcs] + [k[:, h]], dim=1)
-        vv = torch.cat([inputs[s][2][:, h] for s in srcs] + [v[:, h]], dim=1)
-        z = np.zeros((1, 0), np.int32)
-        o, _ = oattn.flat_segmented_attention(
-            to_np(q[:, h:h + 1]), None, None, z, z, np.zeros(1, np.int32),
-            to_np(kk[:, None]), to_np(vv[:, None]), scale, batches=batches)
-        out[:, :, h * D:(h + 1) * D] = o
-    return out
 
 
 @pytest.mark.parametrize("layer,fused", [(0, "1"), (29, "1"), (0, "0")])
@@ -72,16 +55,13 @@ def test_generation_under_reference_policy(device, monkeypatch, layer, fused):
     for t, (q, k, v) in enumerate(inputs):
         out = cache.step(q.to(device), k.to(device), v.to(device), t, scale)
         torch.cuda.synchronize(device)
-        # every head; at the large scales batch row 1 only (the oracle's time)
-        big = q.shape[2] >= 1600
-        heads = list(range(H))
-        batches = [1] if big else None
-        ref = _reference(inputs, ctrl, layer, t, scale, heads, batches)
+        ref, _ = kept_keys_reference(inputs, lambda h: _kept_sources(ctrl, layer, t, h), t, scale)
         o = to_np(out)
-        bs = batches if batches is not None else list(range(B))
-        for h in heads:
-            sl = slice(h * 128, (h + 1) * 128)
-            assert_attention_close(o[bs][:, :, sl], None, ref[bs][:, :, sl], None, what=f"layer {layer} step {t} h {h}")
+        for b in range(B):
+            for h in range(H):
+                sl = slice(h * 128, (h + 1) * 128)
+                assert_attention_close(o[b, :, sl], None, ref[b, :, sl], None,
+                                       what=f"layer {layer} step {t} b {b} h {h}")
         if cache.active and t + 1 < len(SIDES_1M):
             slab_k, slab_v = bits(cache.cached_k), bits(cache.cached_v)
             for seg in sched.live_segments(t + 1):
