@@ -307,10 +307,20 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(device)
-    t0.record(stream)
-    for _ in range(images):
-        image()
-    t1.record(stream)
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        host0 = time.perf_counter()
+        t0.record(stream)
+        for _ in range(images):
+            image()
+        t1.record(stream)
+        # host time to enqueue one layer-step (SegmentedLayerCache.step:
+        # replayed steps after the first image)
+        host_us_step = (time.perf_counter() - host0) / (images * layers * len(sides)) * 1e6
+    finally:
+        if gc_was_on:
+            gc.enable()
     torch.cuda.synchronize(device)
     ms = t0.elapsed_time(t1) / images
     # the same image captured in one HIP graph (all 416 layer-steps): replays
@@ -374,7 +384,8 @@ def time_sweep(device, images, layers=32, heads=16, batch=2):
         prof.set_real_pruning_fast_phase_profile_enabled(False)
     return dict(what=f"{layers} layers x {len(sides)} scale steps, B={batch}, H={heads}, budget 0.1, "
                      "static per-layer keep policies (seed 1000 + layer)",
-                ms_per_image=round(ms, 3), ms_per_image_graph=round(ms_graph, 3), attention_flops=flops,
+                ms_per_image=round(ms, 3), ms_per_image_graph=round(ms_graph, 3),
+                host_us_per_layer_step=round(host_us_step, 2), attention_flops=flops,
                 tflops=round(flops / (ms * 1e-3) / 1e12, 1),
                 per_scale_step=per_step, graph_kernel_floor_us=round(floor_us, 2),
                 phase_gpu_ms_profiled={k: round(v, 3) for k, v in snap["cuda_ms"].items()},

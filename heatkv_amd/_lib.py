@@ -71,6 +71,13 @@ SIGNATURES = {
          _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
          _c_i32, _c_p, _c_i32, _c_p],
     ),
+    "hkv_segmented_attention_bound_bytes": (_c_i64, []),
+    "hkv_segmented_attention_bind": (
+        _c_i32,
+        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+         _c_i32, ctypes.c_float, _c_i32, _c_i32, _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p],
+    ),
+    "hkv_segmented_attention_call": (_c_i32, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "hkv_segmented_attention_plan": (
         _c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i32]),
     "hkv_segmented_attention_item_shape": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),

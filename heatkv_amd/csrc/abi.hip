@@ -178,17 +178,21 @@ int32_t hkv_segmented_attention(const void* q, const void* slab_k, const void* s
                                         workspace, workspace_bytes, nullptr, stream);
 }
 
-int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v,
-                                       const int32_t* seg_starts, const int32_t* seg_ends,
-                                       const int32_t* seg_counts, const void* cur_k, const void* cur_v,
-                                       void* out, float* lse, int32_t batch, int32_t heads,
-                                       int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
-                                       int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
-                                       int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
-                                       int32_t qk_dot_mode, int32_t value_dot_mode,
-                                       const int32_t* work_plan, int32_t plan_units,
-                                       void* workspace, int64_t workspace_bytes, const int32_t* append_offsets,
-                                       void* stream) {
+// Validates the arguments of hkv_segmented_attention_append and fills `a`
+// (0 or a negative HKV_ERR_* code with the message set).  With
+// `check_tensors` false the tensor pointers (q, slab, current K/V, out) are
+// not looked at: hkv_segmented_attention_bind checks them at each call.
+namespace {
+int32_t build_attention_args(hkv::AttnArgs& a, bool check_tensors, const void* q, void* slab_k, void* slab_v,
+                                      const int32_t* seg_starts, const int32_t* seg_ends,
+                                      const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                      void* out, float* lse, int32_t batch, int32_t heads,
+                                      int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                      int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                      int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                      int32_t qk_dot_mode, int32_t value_dot_mode,
+                                      const int32_t* work_plan, int32_t plan_units,
+                                      void* workspace, int64_t workspace_bytes, const int32_t* append_offsets) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (qk_dot_mode < 0 || qk_dot_mode > 2)
     return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
@@ -230,9 +234,10 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
   if (slab_capacity * static_cast<int64_t>(max_segments > 0 ? max_segments : 1) + cur_len >
       0x7fffffffLL)
     return fail(HKV_ERR_UNSUPPORTED, "slab_capacity * max_segments + current_len exceeds 2^31");
-  if (!q || !cur_k || !cur_v || !out || !seg_counts || (max_segments > 0 && (!seg_starts || !seg_ends)))
+  if (!seg_counts || (max_segments > 0 && (!seg_starts || !seg_ends)) ||
+      (check_tensors && (!q || !cur_k || !cur_v || !out)))
     return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
-  if (slab_capacity > 0 && (!slab_k || !slab_v))
+  if (check_tensors && slab_capacity > 0 && (!slab_k || !slab_v))
     return fail(HKV_ERR_INVALID_ARG, "null slab pointer with nonzero capacity");
   if (workspace != nullptr) {
     if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
@@ -256,11 +261,11 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
     // the copy moves whole rows 16 bytes per access
     const uintptr_t bits = reinterpret_cast<uintptr_t>(slab_k) | reinterpret_cast<uintptr_t>(slab_v) |
                            reinterpret_cast<uintptr_t>(cur_k) | reinterpret_cast<uintptr_t>(cur_v);
-    if (slab_capacity < cur_len || (bits & 15) != 0)
+    if (slab_capacity < cur_len || (check_tensors && (bits & 15) != 0))
       return fail(HKV_ERR_INVALID_ARG,
                   "the append needs slab_capacity >= current_len and 16-byte aligned slab and current tensors");
   }
-  hkv::AttnArgs a{};
+  a = hkv::AttnArgs{};
   a.q = q;
   a.slab_k = slab_k;
   a.slab_v = slab_v;
@@ -288,6 +293,89 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
   a.plan = work_plan;
   a.plan_units = work_plan != nullptr ? plan_units : 0;
   a.append_offsets = append_offsets;
+  return 0;
+}
+}  // namespace
+
+int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v,
+                                      const int32_t* seg_starts, const int32_t* seg_ends,
+                                      const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                      void* out, float* lse, int32_t batch, int32_t heads,
+                                      int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                      int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                      int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                      int32_t qk_dot_mode, int32_t value_dot_mode,
+                                      const int32_t* work_plan, int32_t plan_units,
+                                      void* workspace, int64_t workspace_bytes, const int32_t* append_offsets,
+                                       void* stream) {
+  hkv::AttnArgs a{};
+  const int32_t code = build_attention_args(
+      a, true, q, slab_k, slab_v, seg_starts, seg_ends, seg_counts, cur_k, cur_v, out, lse, batch, heads, cur_len,
+      slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype, softmax_scale, use_exp2,
+      qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes, append_offsets);
+  if (code != 0) return code;
+  const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+// The argument block of hkv_segmented_attention_bind: the validated launch
+// arguments, the device they were validated for and a tag.
+namespace {
+constexpr uint32_t kBoundTag = 0x484b5641u;
+struct BoundAttention {
+  uint32_t tag;
+  int32_t device;
+  hkv::AttnArgs a;
+};
+}  // namespace
+
+int64_t hkv_segmented_attention_bound_bytes(void) { return static_cast<int64_t>(sizeof(BoundAttention)); }
+
+int32_t hkv_segmented_attention_bind(void* bound, int64_t bound_bytes, const int32_t* seg_starts,
+                                     const int32_t* seg_ends, const int32_t* seg_counts, int32_t batch,
+                                     int32_t heads, int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                     int32_t head_dim, int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                     int32_t out_dtype, float softmax_scale, int32_t use_exp2, int32_t qk_dot_mode,
+                                     int32_t value_dot_mode, const int32_t* work_plan, int32_t plan_units,
+                                     void* workspace, int64_t workspace_bytes, const int32_t* append_offsets) {
+  if (bound == nullptr || bound_bytes < static_cast<int64_t>(sizeof(BoundAttention)) ||
+      (reinterpret_cast<uintptr_t>(bound) & 7) != 0)
+    return fail(HKV_ERR_INVALID_ARG, "bound must point to %d bytes, 8-byte aligned (hkv_segmented_attention_bound_bytes)",
+                static_cast<int>(sizeof(BoundAttention)));
+  BoundAttention* b = static_cast<BoundAttention*>(bound);
+  b->tag = 0;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
+  const int32_t code = build_attention_args(
+      b->a, false, nullptr, nullptr, nullptr, seg_starts, seg_ends, seg_counts, nullptr, nullptr, nullptr, nullptr,
+      batch, heads, cur_len, slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype,
+      softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes,
+      append_offsets);
+  if (code != 0) return code;
+  b->device = device;
+  b->tag = kBoundTag;
+  return ok();
+}
+
+int32_t hkv_segmented_attention_call(const void* bound, const void* q, void* slab_k, void* slab_v,
+                                     const void* cur_k, const void* cur_v, void* out, void* stream) {
+  const BoundAttention* b = static_cast<const BoundAttention*>(bound);
+  if (b == nullptr || b->tag != kBoundTag) return fail(HKV_ERR_INVALID_ARG, "not a bound attention call");
+  if (!q || !cur_k || !cur_v || !out || (b->a.slab_capacity > 0 && (!slab_k || !slab_v)))
+    return fail(HKV_ERR_INVALID_ARG, "null pointer argument");
+  if (b->a.append_offsets != nullptr &&
+      ((reinterpret_cast<uintptr_t>(slab_k) | reinterpret_cast<uintptr_t>(slab_v) |
+        reinterpret_cast<uintptr_t>(cur_k) | reinterpret_cast<uintptr_t>(cur_v)) & 15) != 0)
+    return fail(HKV_ERR_INVALID_ARG, "the append needs 16-byte aligned slab and current tensors");
+  hkv::AttnArgs a = b->a;
+  a.q = q;
+  a.slab_k = slab_k;
+  a.slab_v = slab_v;
+  a.cur_k = cur_k;
+  a.cur_v = cur_v;
+  a.out = out;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));

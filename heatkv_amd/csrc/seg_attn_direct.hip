@@ -40,8 +40,10 @@ __device__ __forceinline__ u32x2_t ds_read_tr(const uint8_t* p) {
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p)));
 }
 
-// 16-byte-per-lane buffer load written straight to LDS at `lds_addr` (the
-// wave-uniform LDS byte address; lane l lands at lds_addr + 16 l).  Issued as
+// 16-byte-per-lane buffer load of byte offset voff + IMM of `rsrc`, written
+// straight to LDS at `lds_addr` (the wave-uniform LDS byte address; lane l
+// lands at lds_addr + 16 l); the add rides in the same asm, so the compiler
+// keeps one offset register per wave, not one per DMA instruction.  Issued as
 // inline assembly so that the compiler, which cannot see the LDS write, does
 // not make every later LDS read wait for all outstanding loads: ordering is
 // explicit here (s_waitcnt vmcnt before each tile's barrier).
@@ -50,11 +52,20 @@ __device__ __forceinline__ u32x2_t ds_read_tr(const uint8_t* p) {
 // compiler's warning about clobbering a reserved register is silenced.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const u32x4_t rsrc, uint32_t lds_addr, int32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
+template <int IMM>
+__device__ __forceinline__ void dma16_at(const u32x4_t rsrc, uint32_t lds_addr, int32_t voff) {
+  if constexpr (IMM == 0) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+  } else {
+    int32_t tmp;
+    asm volatile("v_add_u32_e32 %0, %4, %2\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %3, 0 offen lds"
+                 : "=&v"(tmp)
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc), "i"(IMM)
+                 : "memory", "m0");
+  }
 }
 #pragma clang diagnostic pop
 
@@ -175,24 +186,21 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   const uint32_t cur_bytes = static_cast<uint32_t>(L * kD * 2);
   constexpr int32_t kPastEnd = static_cast<int32_t>(0x80000000u);
 
-  int dma_key[kDmaPerWave];
-  int dma_col[kDmaPerWave];
-  int dma_off[kDmaPerWave];
-#pragma unroll
-  for (int i = 0; i < kDmaPerWave; ++i) {
-    const int q = wave * kDmaPerWave + i;
-    if (k_wave) {
-      dma_key[i] = (q >> 3) * 32 + (lane & 31);
-      dma_col[i] = (q & 7) * 32 + (lane >> 5) * 16;
-    } else {
-      const int qv = q - 16;
-      const int lp = lane & 31;
-      const int db = 2 * (qv & 1) + (lane >> 5);
-      dma_key[i] = 16 * (qv >> 2) + 8 * ((qv >> 1) & 1) + 4 * (lp >> 4) + ((lp & 7) >> 1);
-      dma_col[i] = 2 * (db * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
-    }
-    dma_off[i] = dma_key[i] * (kD * 2) + dma_col[i];
+  // DMA i of a tile moves 32 key rows x 32 bytes (K waves: K block (wave, i))
+  // or 8 key rows x 128 bytes (V waves); the lane's key row and byte column
+  // follow from DMA 0's by constants: K key + 0, column + 32 i; V key +
+  // 16 (i >> 2) + 8 ((i >> 1) & 1), column + 128 (i & 1).
+  static_assert(kDmaPerWave == 8, "DMA pattern");
+  int key0, col0;
+  if (k_wave) {
+    key0 = wave * 32 + (lane & 31);
+    col0 = (lane >> 5) * 16;
+  } else {
+    const int lp = lane & 31;
+    key0 = 32 * (wave - 2) + 4 * (lp >> 4) + ((lp & 7) >> 1);
+    col0 = 2 * ((lane >> 5) * 32 + 16 * ((lp >> 3) & 1) + 8 * (lp & 1));
   }
+  const int32_t off0 = key0 * (kD * 2) + col0;
   const uint32_t ring_lds = lds_address(ring) + wave * kDmaPerWave * 1024;
 
   // This wave's tensor (K or V) of current-scale tile c into stage c % 2.
@@ -200,8 +208,25 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     const uint32_t dst = ring_lds + (c % NS) * kStageBytes;
     const uint32_t skip = static_cast<uint32_t>(c) * (kBN * kD * 2);
     const u32x4_t d_cur = make_desc(cur_base + skip, cur_bytes - skip);
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) dma16(d_cur, dst + i * 1024, dma_off[i]);
+    if (k_wave) {
+      dma16_at<0>(d_cur, dst, off0);
+      dma16_at<32>(d_cur, dst + 1024, off0);
+      dma16_at<64>(d_cur, dst + 2048, off0);
+      dma16_at<96>(d_cur, dst + 3072, off0);
+      dma16_at<128>(d_cur, dst + 4096, off0);
+      dma16_at<160>(d_cur, dst + 5120, off0);
+      dma16_at<192>(d_cur, dst + 6144, off0);
+      dma16_at<224>(d_cur, dst + 7168, off0);
+    } else {
+      dma16_at<0>(d_cur, dst, off0);
+      dma16_at<128>(d_cur, dst + 1024, off0);
+      dma16_at<2048>(d_cur, dst + 2048, off0);
+      dma16_at<2176>(d_cur, dst + 3072, off0);
+      dma16_at<4096>(d_cur, dst + 4096, off0);
+      dma16_at<4224>(d_cur, dst + 5120, off0);
+      dma16_at<6144>(d_cur, dst + 6144, off0);
+      dma16_at<6272>(d_cur, dst + 7168, off0);
+    }
   };
   // A planned unit whose first tile is a current-scale one (every whole item,
   // and a part that starts there) issues it before the head's segment tables
@@ -267,8 +292,28 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     const int p = tile - ntc;
     const uint32_t dst = ring_lds + (tile % NS) * kStageBytes;
     const int32_t* rt = rowtab[p % 3];
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) dma16(d_prior, dst + i * 1024, rt[dma_key[i]] + dma_col[i]);
+    if (k_wave) {
+      const int32_t r = rt[key0] + col0;
+      dma16_at<0>(d_prior, dst, r);
+      dma16_at<32>(d_prior, dst + 1024, r);
+      dma16_at<64>(d_prior, dst + 2048, r);
+      dma16_at<96>(d_prior, dst + 3072, r);
+      dma16_at<128>(d_prior, dst + 4096, r);
+      dma16_at<160>(d_prior, dst + 5120, r);
+      dma16_at<192>(d_prior, dst + 6144, r);
+      dma16_at<224>(d_prior, dst + 7168, r);
+    } else {
+      const int32_t r0 = rt[key0] + col0, r1 = rt[key0 + 8] + col0;
+      const int32_t r2 = rt[key0 + 16] + col0, r3 = rt[key0 + 24] + col0;
+      dma16_at<0>(d_prior, dst, r0);
+      dma16_at<128>(d_prior, dst + 1024, r0);
+      dma16_at<0>(d_prior, dst + 2048, r1);
+      dma16_at<128>(d_prior, dst + 3072, r1);
+      dma16_at<0>(d_prior, dst + 4096, r2);
+      dma16_at<128>(d_prior, dst + 5120, r2);
+      dma16_at<0>(d_prior, dst + 6144, r3);
+      dma16_at<128>(d_prior, dst + 7168, r3);
+    }
   };
   auto valid_of = [&](int t) { return t < ntc ? min(kBN, L - t * kBN) : min(kBN, R - (t - ntc) * kBN); };
 

@@ -336,6 +336,7 @@ def fused_real_pruning_flat_segmented_attention(
     work_plan: Optional[torch.Tensor] = None,
     append_offsets: Optional[torch.Tensor] = None,
     k_split_rows: bool = False,
+    _bind: Optional[list] = None,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
 
@@ -355,7 +356,9 @@ def fused_real_pruning_flat_segmented_attention(
     ``k_split_rows`` (an extension): q is fp32 and ``current_k`` /
     ``persisted_k`` are float32-typed tensors whose rows hold split rows of
     fp32 K (:func:`qkv_produce` with ``k_split_rows=True``), so the call skips
-    its own split of K; same results as passing the fp32 K.
+    its own split of K; same results as passing the fp32 K.  ``_bind``
+    (internal): a list that receives what :class:`BoundSegmentedAttention`
+    needs to repeat this launch.
     Mirrors fused_real_pruning_flat_segmented_attention
     (real_pruning_fused_attention.py:445-591); the work is the HIP kernel
     ``hkv_segmented_attention``.
@@ -427,7 +430,8 @@ def fused_real_pruning_flat_segmented_attention(
         _positive_int_env(knob, default)
     qk_mode = _fused_qk_dot_mode_id()
     value_mode = _fused_value_dot_mode_id()
-    if q.dtype != current_k.dtype and not k_split_rows:
+    promoted = q.dtype != current_k.dtype and not k_split_rows
+    if promoted:
         q, persisted_k, current_k = _promote_mixed_qk(q, persisted_k, current_k, qk_mode, append_offsets)
 
     _lib.require_device(q.device)
@@ -482,13 +486,14 @@ def fused_real_pruning_flat_segmented_attention(
     stream = torch.cuda.current_stream(q.device)
     ws = _lib.attention_workspace(q.device, stream)
     k_code = _lib.dtype_code(current_k.dtype)
+    converted = promoted or (split and not k_split_rows)
     if split:
         # fp32 K as split rows for the split-row kernel (the q split happens in it)
         if not k_split_rows:
             persisted_k = _split_rows(persisted_k, stream)
             current_k = _split_rows(current_k, stream)
         k_code = _lib.DTYPE_SPLIT_ROWS
-    args = (
+    args = [
         q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
         segment_starts.data_ptr(), segment_ends.data_ptr(), segment_counts.data_ptr(),
         current_k.data_ptr(), current_v.data_ptr(), output.data_ptr(),
@@ -500,12 +505,98 @@ def fused_real_pruning_flat_segmented_attention(
         work_plan.data_ptr() if work_plan is not None else None,
         int(work_plan.shape[0]) if work_plan is not None else 0,
         ws.data_ptr() if ws is not None else None, int(ws.numel()) if ws is not None else 0,
-    )
+    ]
+    lib = _lib.load()
     if append_offsets is None:
-        code = _lib.load().hkv_segmented_attention(*args, stream.cuda_stream)
+        fn = lib.hkv_segmented_attention
     else:
-        code = _lib.load().hkv_segmented_attention_append(*args, append_offsets.data_ptr(), stream.cuda_stream)
-    _lib.check(code)
+        fn = lib.hkv_segmented_attention_append
+        args.append(append_offsets.data_ptr())
+    args.append(stream.cuda_stream)
+    _lib.check(fn(*args))
+    if _bind is not None:
+        # what a pre-bound call needs to repeat this launch for new q / k / v
+        # / slab tensors of the same shapes (None when this call converted its
+        # inputs: those copies are per call)
+        keep = (q, persisted_k, persisted_v, current_k, current_v, segment_starts, segment_ends, segment_counts,
+                work_plan, append_offsets, ws)
+        _bind.append(None if converted or lse is not None else (fn, args, output.shape, out_dtype, keep))
     if return_lse:
         return output, lse
     return output
+
+
+class BoundSegmentedAttention:
+    """A pre-validated launch of :func:`fused_real_pruning_flat_segmented_attention`
+    for callers that repeat one call shape many times (the segmented cache's
+    per-(layer, scale) steps): built from one call of the operator (which runs
+    every check), it holds that call's arguments bound in the library
+    (``hkv_segmented_attention_bind``) and repeats the launch
+    (``hkv_segmented_attention_call``) for new q, current K/V and slab tensors
+    with the same shapes, dtypes and device, on the same stream, with the same
+    tables, plan, append offsets and knobs: the operator's validation and
+    argument marshalling are skipped, only the new tensors' pointers pass.
+    ``__call__`` returns None, launching nothing, when the new tensors or the
+    stream do not match (or a HIP graph is being captured); the caller then
+    calls the operator."""
+
+    __slots__ = ("_block", "_addr", "_call", "_out_shape", "_out_dtype", "_keep", "_dev", "_device", "_stream",
+                 "_qs", "_ps", "_qdt", "_kdt", "_vdt", "_skdt", "_svdt")
+
+    def __init__(self, record, *, q, current_k, current_v, persisted_k, persisted_v):
+        import ctypes
+
+        fn, a, out_shape, out_dtype, keep = record
+        lib = _lib.load()
+        size = int(lib.hkv_segmented_attention_bound_bytes())
+        self._block = (ctypes.c_int64 * ((size + 7) // 8))()
+        self._addr = ctypes.addressof(self._block)
+        append = a[28] if len(a) > 29 else None
+        _lib.check(lib.hkv_segmented_attention_bind(
+            self._addr, size, a[3], a[4], a[5], a[10], a[11], a[12], a[13], a[14], a[15], a[16], a[17], a[18],
+            a[19], a[20], a[21], a[22], a[23], a[24], a[25], a[26], a[27], append))
+        self._call = lib.hkv_segmented_attention_call
+        self._out_shape = tuple(out_shape)
+        self._out_dtype = out_dtype
+        self._keep = keep  # tables, plan, offsets and workspace the bound pointers refer to
+        self._dev = q.get_device()
+        self._device = q.device
+        self._stream = a[-1]
+        self._qs = q.shape
+        self._ps = persisted_k.shape
+        self._qdt, self._kdt, self._vdt = q.dtype, current_k.dtype, current_v.dtype
+        self._skdt, self._svdt = persisted_k.dtype, persisted_v.dtype
+
+    @classmethod
+    def bind(cls, **kwargs):
+        """Calls the operator with ``kwargs`` and returns ``(output, bound)``;
+        ``bound`` is None when the call cannot be repeated this way (its
+        inputs were converted for the launch, or it returned the LSE)."""
+        rec = []
+        out = fused_real_pruning_flat_segmented_attention(**kwargs, _bind=rec)
+        bound = None
+        if rec and rec[0] is not None and not torch.cuda.is_current_stream_capturing():
+            bound = cls(rec[0], q=kwargs["q"], current_k=kwargs["current_k"], current_v=kwargs["current_v"],
+                        persisted_k=kwargs["persisted_k"], persisted_v=kwargs["persisted_v"])
+        return out, bound
+
+    def __call__(self, q, current_k, current_v, persisted_k, persisted_v):
+        qs, ps, dev = self._qs, self._ps, self._dev
+        if (q.shape != qs or current_k.shape != qs or current_v.shape != qs or persisted_k.shape != ps
+                or persisted_v.shape != ps or q.dtype is not self._qdt or current_k.dtype is not self._kdt
+                or current_v.dtype is not self._vdt or persisted_k.dtype is not self._skdt
+                or persisted_v.dtype is not self._svdt or q.get_device() != dev or current_k.get_device() != dev
+                or current_v.get_device() != dev or persisted_k.get_device() != dev
+                or persisted_v.get_device() != dev or not q.is_contiguous() or not current_k.is_contiguous()
+                or not current_v.is_contiguous() or not persisted_k.is_contiguous()
+                or not persisted_v.is_contiguous()):
+            return None
+        stream = torch._C._cuda_getCurrentRawStream(dev)
+        if stream != self._stream or torch.cuda.is_current_stream_capturing():
+            return None
+        out = torch.empty(self._out_shape, dtype=self._out_dtype, device=self._device)
+        code = self._call(self._addr, q.data_ptr(), persisted_k.data_ptr(), persisted_v.data_ptr(),
+                          current_k.data_ptr(), current_v.data_ptr(), out.data_ptr(), stream)
+        if code != 0:
+            _lib.check(code)
+        return out

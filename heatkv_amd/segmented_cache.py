@@ -35,6 +35,7 @@ import torch
 
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
+    BoundSegmentedAttention,
     attention_fuses_append,
     attention_queries_per_item,
     concat_kv,
@@ -92,6 +93,82 @@ def has_removed(removed: Mapping[int, Set[int]]) -> bool:
     return any(len(v) > 0 for v in removed.values())
 
 
+# Environment knobs a step's launches depend on; a cache replays recorded
+# steps only while they read as they did when the steps were recorded (they
+# are read once per generation, at its first step).
+_STEP_KNOBS = ("REAL_PRUNING_FUSED_QK_DOT_MODE", "REAL_PRUNING_FUSED_VALUE_DOT_MODE",
+               "REAL_PRUNING_FUSED_SOFTMAX_MODE", "REAL_PRUNING_FUSED_SEGMENTED_BASELINE_PREFIX",
+               "REAL_PRUNING_FUSED_BLOCK_M", "REAL_PRUNING_FUSED_BLOCK_N", "REAL_PRUNING_FUSED_NUM_WARPS",
+               "REAL_PRUNING_FUSED_NUM_STAGES", "HKV_ATTN_SPLIT", "HKV_ATTN_PLAN", "HKV_FUSED_APPEND",
+               "HKV_ATTN_SPLIT_ROWS")
+
+
+class _StepReplay:
+    """One recorded step of a generation (scale, shapes, dtypes and arguments
+    fixed), repeated by later generations without the step's host logic: the
+    attention launch through a :class:`BoundSegmentedAttention` and the state
+    changes that followed it.  ``run`` returns None (doing nothing) when the
+    cache is not in the state the step was recorded in, or the launch cannot
+    be repeated as bound; the caller then takes the full step."""
+
+    __slots__ = ("args", "kind", "attn", "old_len", "new_len", "final", "k_split_rows", "copy", "activate",
+                 "buf_shapes")
+
+    def __init__(self, args, kind, attn, old_len, new_len, final, copy=None, activate=None, buf_shapes=None):
+        self.args = args  # the step's (out_dtype, softmax_scale, softmax_mode, appended, k_split_rows)
+        k_split_rows = bool(args[4])
+        self.kind = kind  # "slab": segmented step; "dense": dense prefix kept in place
+        self.attn = attn
+        self.old_len = old_len
+        self.new_len = new_len
+        self.final = final
+        self.k_split_rows = k_split_rows
+        self.copy = copy  # (plan, tag) of the residual append, or None
+        self.activate = activate  # target whose slab is packed after a dense step, or None
+        self.buf_shapes = buf_shapes  # ((shape, dtype), (shape, dtype)) of the dense buffer
+
+    def run(self, cache: "SegmentedLayerCache", q, k, v):
+        if cache.logical_len != self.old_len:
+            return None
+        if self.old_len == 0:
+            cache.k_split_rows = self.k_split_rows
+        elif cache.k_split_rows != self.k_split_rows:
+            return None
+        if self.kind == "slab":
+            if not cache.active or cache.cached_k is None:
+                return None
+            out = self.attn(q, k, v, cache.cached_k, cache.cached_v)
+            if out is None:
+                return None
+            if self.final:
+                cache.reset()
+                return out
+            if self.copy is not None:
+                cache._copy(self.copy[0], k, v, self.copy[1])
+            cache.logical_len = self.new_len
+            return out
+        if cache.active:
+            return None
+        if cache.dense_buf is None:
+            if self.old_len != 0:
+                return None
+            (sk, dk), (sv, dv) = self.buf_shapes
+            cache.dense_buf = (torch.empty(sk, dtype=dk, device=k.device), torch.empty(sv, dtype=dv, device=v.device))
+        buf_k, buf_v = cache.dense_buf
+        B, H, cap = buf_k.shape[0], buf_k.shape[1], buf_k.shape[2]
+        out = self.attn(q, k, v, buf_k.view(B, H * cap, buf_k.shape[3]), buf_v.view(B, H * cap, buf_v.shape[3]))
+        if out is None:
+            return None
+        if self.final:
+            cache.reset()
+            return out
+        cache.logical_len = self.new_len
+        if self.activate is not None:
+            cache._activate_from_dense(buf_k, buf_v, self.activate)
+            cache.dense_buf = None
+        return out
+
+
 class SegmentedLayerCache:
     """KV cache of one attention layer under a static slab schedule."""
 
@@ -103,6 +180,9 @@ class SegmentedLayerCache:
         self.num_scales = int(schedule.num_scales if num_scales is None else num_scales)
         self._tables_by_len: Dict[tuple, Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
         self._dense_current_plans: Dict[tuple, Tuple[CopyPlan, CopyPlan]] = {}
+        # steps recorded by an earlier generation, by scale
+        self._replays: Dict[int, _StepReplay] = {}
+        self._knobs: Optional[tuple] = None
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -230,7 +310,8 @@ class SegmentedLayerCache:
         return fused_append_enabled() and attention_fuses_append(q.dtype, k.dtype, v.dtype,
                                                                  k_split_rows=self.k_split_rows)
 
-    def _dense_step_in_place(self, q, k, v, scale_ind: int, scale: float, mode, out_dtype, final: bool):
+    def _dense_step_in_place(self, q, k, v, scale_ind: int, scale: float, mode, out_dtype, final: bool,
+                             record=None):
         """A dense-prefix step (:1972-2038) on the in-place buffer: attention over
         the rows so far plus the current scale, whose rows the same launch
         writes behind them (the reference concatenates them onto the cache);
@@ -249,22 +330,32 @@ class SegmentedLayerCache:
             raise RuntimeError("dense prefix longer than its in-place buffer")
         qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows)
         st, en, ct, plan, offs = self._in_place_tables(H, cap, old_len, q.device, B, L, qpi, store)
+        kw = dict(q=q, persisted_k=buf_k.reshape(B, H * cap, buf_k.shape[3]),
+                  persisted_v=buf_v.reshape(B, H * cap, buf_v.shape[3]), segment_starts=st, segment_ends=en,
+                  segment_counts=ct, current_k=k, current_v=v, softmax_scale=scale, softmax_mode=mode,
+                  out_dtype=out_dtype, work_plan=plan, append_offsets=offs, k_split_rows=self.k_split_rows)
+        bound = None
         with prof.phase("attention"):
-            out = fused_real_pruning_flat_segmented_attention(
-                q=q, persisted_k=buf_k.reshape(B, H * cap, buf_k.shape[3]),
-                persisted_v=buf_v.reshape(B, H * cap, buf_v.shape[3]), segment_starts=st, segment_ends=en,
-                segment_counts=ct, current_k=k, current_v=v, softmax_scale=scale, softmax_mode=mode,
-                out_dtype=out_dtype, work_plan=plan, append_offsets=offs, k_split_rows=self.k_split_rows)
+            if record is not None:
+                out, bound = BoundSegmentedAttention.bind(**kw)
+            else:
+                out = fused_real_pruning_flat_segmented_attention(**kw)
+        activate = None
         if final:
             self.reset()
-            return out
-        self.logical_len = old_len + L
-        if has_removed(self.removed(scale_ind + 1)):
-            if self.logical_len != cap:
-                raise RuntimeError("dense prefix packed into the slab before its buffer is full")
-            with prof.phase("compact"):
-                self._activate_from_dense(buf_k, buf_v, scale_ind + 1)
-            self.dense_buf = None
+        else:
+            self.logical_len = old_len + L
+            if has_removed(self.removed(scale_ind + 1)):
+                if self.logical_len != cap:
+                    raise RuntimeError("dense prefix packed into the slab before its buffer is full")
+                activate = scale_ind + 1
+                with prof.phase("compact"):
+                    self._activate_from_dense(buf_k, buf_v, activate)
+                self.dense_buf = None
+        if bound is not None:
+            self._replays[scale_ind] = _StepReplay(
+                record, "dense", bound, old_len, old_len + L, final,
+                activate=activate, buf_shapes=((tuple(buf_k.shape), buf_k.dtype), (tuple(buf_v.shape), buf_v.dtype)))
         return out
 
     # ------------------------------------------------------------------ attention
@@ -356,6 +447,21 @@ class SegmentedLayerCache:
         ``k_split_rows``: k (fp32-typed) holds split rows of fp32 K
         (``qkv_produce(..., k_split_rows=True)``); every step of a generation
         passes the same value, and the cache's K rows keep that format."""
+        record = None
+        if not prof.phase_profile_enabled():
+            if self.logical_len == 0:
+                knobs = tuple(os.environ.get(n) for n in _STEP_KNOBS)
+                if knobs != self._knobs:
+                    self._replays.clear()
+                    self._knobs = knobs
+            record = (out_dtype, softmax_scale, softmax_mode, appended, k_split_rows)
+            rp = self._replays.get(scale_ind)
+            if rp is not None and rp.args == record:
+                out = rp.run(self, q, k, v)
+                if out is not None:
+                    return out
+            if not q.is_cuda or _capturing():
+                record = None  # record eager GPU steps only
         if appended and not self.active:
             raise RuntimeError("appended=True needs an active slab (see producer_append)")
         if self.logical_len == 0:
@@ -371,7 +477,8 @@ class SegmentedLayerCache:
         if baseline_prefix_enabled() and not self.active and not has_removed(self.removed(scale_ind)):
             # dense prefix (:1972-2038)
             if self.dense_buf is not None or (old_len == 0 and self._in_place_ok(q, k, v)):
-                return self._dense_step_in_place(q, k, v, scale_ind, softmax_scale, mode, out_dtype, final)
+                return self._dense_step_in_place(q, k, v, scale_ind, softmax_scale, mode, out_dtype, final,
+                                                 record)
             with prof.phase("attention"):
                 out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
             if final:
@@ -393,6 +500,7 @@ class SegmentedLayerCache:
 
         dense_candidate = None
         fused = False
+        bound = None
         if old_len == 0:
             with prof.phase("attention"):
                 out = self._attend_dense(q, k, v, softmax_scale, mode, out_dtype)
@@ -403,6 +511,7 @@ class SegmentedLayerCache:
                 dense_candidate = concat_kv(self.cached_k, k, self.cached_v, v)
                 prof.stat_add("dense_attention_cat_calls")
         else:
+            was_active = self.active
             with prof.phase("materialize"):
                 if not self.active:
                     self._activate_from_dense(self.cached_k, self.cached_v, scale_ind)
@@ -415,17 +524,22 @@ class SegmentedLayerCache:
                         if work_plans_enabled(q.device) else None)
                 offsets = None if final or appended else self._fused_append_offsets(scale_ind, q, k, v)
                 fused = offsets is not None
+            kw = dict(q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
+                      segment_starts=starts, segment_ends=ends, segment_counts=counts,
+                      current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
+                      out_dtype=out_dtype, work_plan=plan, append_offsets=offsets,
+                      k_split_rows=self.k_split_rows)
             with prof.phase("attention"):
-                out = fused_real_pruning_flat_segmented_attention(
-                    q=q, persisted_k=self.cached_k, persisted_v=self.cached_v,
-                    segment_starts=starts, segment_ends=ends, segment_counts=counts,
-                    current_k=k, current_v=v, softmax_scale=softmax_scale, softmax_mode=mode,
-                    out_dtype=out_dtype, work_plan=plan, append_offsets=offsets,
-                    k_split_rows=self.k_split_rows)
+                if record is not None and was_active:
+                    out, bound = BoundSegmentedAttention.bind(**kw)
+                else:
+                    out = fused_real_pruning_flat_segmented_attention(**kw)
 
         with prof.phase("compact"):
             if final:
                 self.reset()
+                if bound is not None:
+                    self._replays[scale_ind] = _StepReplay(record, "slab", bound, old_len, logical, True)
                 return out
             nxt = self.removed(scale_ind + 1)
             if not self.active and not has_removed(nxt):
@@ -447,6 +561,10 @@ class SegmentedLayerCache:
                     tag = ("append", int(scale_ind))
                 if plan is not None:
                     self._copy(plan, k, v, tag)
+                if bound is not None:
+                    self._replays[scale_ind] = _StepReplay(
+                        record, "slab", bound, old_len, logical, False,
+                        copy=(plan, tag) if plan is not None and len(plan) > 0 else None)
             else:
                 # pack the dense cache and the current scale into a new slab (:1713-1789)
                 dense_k, dense_v = self.cached_k, self.cached_v

@@ -193,6 +193,30 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
                                        void* workspace, int64_t workspace_bytes,
                                        const int32_t* append_offsets, void* stream);
 
+/* A bound attention call: hkv_segmented_attention_append's arguments other
+ * than the tensors (tables, shapes, dtypes, scale, dot modes, work plan,
+ * workspace and append offsets) validated once into a caller-owned block of
+ * hkv_segmented_attention_bound_bytes() bytes (8-byte aligned), on the
+ * current device; hkv_segmented_attention_call then launches with new q,
+ * slab K/V, current K/V and output pointers only (no LSE), on `stream`, with
+ * that device current.  The tables, plan, workspace and offsets must stay
+ * valid and unchanged while the block is used; the caller guarantees that the
+ * new tensors have the bound shapes and dtypes (the kernels index them by
+ * those).  No reference counterpart: for callers that repeat one call shape
+ * many times, such as a cache's per-(layer, scale) steps, whose host cost per
+ * launch then drops to the launch itself (the reference re-validates in
+ * Python on every call, real_pruning_fused_attention.py:445-560). */
+int64_t hkv_segmented_attention_bound_bytes(void);
+int32_t hkv_segmented_attention_bind(void* bound, int64_t bound_bytes, const int32_t* seg_starts,
+                                     const int32_t* seg_ends, const int32_t* seg_counts, int32_t batch,
+                                     int32_t heads, int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                     int32_t head_dim, int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                     int32_t out_dtype, float softmax_scale, int32_t use_exp2, int32_t qk_dot_mode,
+                                     int32_t value_dot_mode, const int32_t* work_plan, int32_t plan_units,
+                                     void* workspace, int64_t workspace_bytes, const int32_t* append_offsets);
+int32_t hkv_segmented_attention_call(const void* bound, const void* q, void* slab_k, void* slab_v,
+                                     const void* cur_k, const void* cur_v, void* out, void* stream);
+
 /*
  * Work plan of hkv_segmented_attention for host copies of its offset tables
  * (int32 seg_starts / seg_ends [heads, max_segments], seg_counts [heads]),

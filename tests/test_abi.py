@@ -119,3 +119,18 @@ def test_qkv_produce_argument_errors():
     assert call(stride=100) == _lib.HKV_ERR_INVALID_ARG and "token_stride" in _lib.last_error()
     assert call() == _lib.HKV_ERR_INVALID_ARG and "null" in _lib.last_error()
     assert call(eps=ctypes.c_float(-1.0)) == _lib.HKV_ERR_INVALID_ARG
+
+
+def test_bind_refuses_small_or_unbound_blocks():
+    """The bound-call entry points reject a block that is too small and a
+    block that was never bound, before touching any device."""
+    lib = _lib.load()
+    size = int(lib.hkv_segmented_attention_bound_bytes())
+    assert 64 <= size <= 4096
+    small = (ctypes.c_int64 * 1)()
+    code = lib.hkv_segmented_attention_bind(ctypes.addressof(small), 8, None, None, None, 1, 1, 1, 0, 0, 128,
+                                            2, 2, 2, 0, 1.0, 0, 0, 0, None, 0, None, 0, None)
+    assert code == _lib.HKV_ERR_INVALID_ARG
+    blank = (ctypes.c_int64 * ((size + 7) // 8))()
+    code = lib.hkv_segmented_attention_call(ctypes.addressof(blank), 1, 1, 1, 1, 1, 1, None)
+    assert code == _lib.HKV_ERR_INVALID_ARG
