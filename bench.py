@@ -63,6 +63,12 @@ prints one JSON line.
   scaled_dot_product_attention, fp32) on the host cores over whole steps
   (median of 5 after a warm-up), rank 0 only; ``cores`` = the threads used
   (the per-GPU CPU share), ``host_cpu_count`` = what the OS reports.
+* ``host_us_per_call``: host microseconds to enqueue one headline step
+  through the public operator (every check);
+  ``host_us_per_bound_call``: the same step through its pre-validated launch
+  (BoundSegmentedAttention, what SegmentedLayerCache replays after the first
+  generation); ``sweep.host_us_per_layer_step``: host time per layer-step
+  of the eager sweep images (SegmentedLayerCache.step, replayed).
 * ``clock_ramp_ms``: untimed GPU time of the headline step run before its
   ``--warmup`` (default 300 ms: a cold GPU ramps its clock during the first
   few hundred milliseconds of load).
@@ -190,6 +196,33 @@ def time_attention(kw, device, steps, warmup):
             gc.enable()
     torch.cuda.synchronize(device)
     return t0.elapsed_time(t1) / steps, host_us
+
+
+def time_bound_host(kw, device, steps):
+    """Host microseconds to enqueue one call of the same step through a
+    pre-validated launch (BoundSegmentedAttention: what SegmentedLayerCache
+    replays), the inputs resident on the GPU."""
+    import torch
+
+    from heatkv_amd.real_pruning_fused_attention import BoundSegmentedAttention
+
+    _, bound = BoundSegmentedAttention.bind(**kw)
+    if bound is None:
+        return float("nan")
+    args = (kw["q"], kw["current_k"], kw["current_v"], kw["persisted_k"], kw["persisted_v"])
+    torch.cuda.synchronize(device)
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        host0 = time.perf_counter()
+        for _ in range(steps):
+            bound(*args)
+        host_us = (time.perf_counter() - host0) / steps * 1e6
+    finally:
+        if gc_was_on:
+            gc.enable()
+    torch.cuda.synchronize(device)
+    return host_us
 
 
 def time_attention_median(kw, device, steps, warmup, windows=3):
@@ -721,6 +754,7 @@ def main():
 
     ramp_ms, ramp_launches = clock_ramp(lambda: attn(**kw), device, args.ramp_ms)
     ms_step, host_us = time_attention(kw, device, args.steps, args.warmup)
+    host_us_bound = time_bound_host(kw, device, args.steps)
     achieved = flops / (ms_step * 1e-3)
     pack = time_pack(wl, device)
     if args.copy_calib_mib > 0:
@@ -754,6 +788,7 @@ def main():
         "clock_ramp_ms": round(ramp_ms, 1),
         "clock_ramp_launches": ramp_launches,
         "host_us_per_call": round(host_us, 1),
+        "host_us_per_bound_call": round(host_us_bound, 2),
         "compaction": dict(what=f"slab fill of {wl.name}: one append launch per kept prior scale",
                            **pack),
     }

@@ -231,13 +231,15 @@ def pack_flat_segments_kv(
     lengths: torch.Tensor,
     max_length: Optional[int] = None,
     block_t: int = 32,
+    _bind: Optional[list] = None,
 ):
     """Copy K/V row segments into the slab in place; returns ``(dst_k, dst_v)``.
 
     Item ``i`` copies ``lengths[i]`` rows from ``src[:, src_starts[i]:]`` to
     ``dst[:, dst_starts[i]:]`` for K and V.  Mirrors pack_flat_segments_kv
     (real_pruning_fused_attention.py:365-441); the copy is the HIP kernel
-    ``hkv_pack_segments``.
+    ``hkv_pack_segments``.  ``_bind`` (internal): a list that receives what
+    :class:`BoundPack` needs to repeat this launch.
     """
     for name, tensor in (("dst_k", dst_k), ("dst_v", dst_v), ("src_k", src_k), ("src_v", src_v)):
         if tensor.ndim != 3:
@@ -283,7 +285,7 @@ def pack_flat_segments_kv(
     meta = [t if t.dtype == torch.int64 else t.to(torch.int64) for t in (dst_starts, src_starts, lengths)]
     meta = [t.contiguous() for t in meta]
     n_items = int(meta[0].numel())
-    code = _lib.load().hkv_pack_segments(
+    args = [
         src_k.data_ptr(), src_v.data_ptr(), dst_k.data_ptr(), dst_v.data_ptr(),
         int(src_k.stride(0)), int(dst_k.stride(0)),
         int(src_k.shape[1]), int(dst_k.shape[1]),
@@ -292,8 +294,11 @@ def pack_flat_segments_kv(
         meta[0].data_ptr(), meta[1].data_ptr(), meta[2].data_ptr(),
         n_items, min(row_limit, 2**31 - 1),
         _lib.stream_handle(dst_k.device),
-    )
-    _lib.check(code)
+    ]
+    fn = _lib.load().hkv_pack_segments
+    _lib.check(fn(*args))
+    if _bind is not None:
+        _bind.append((fn, args, meta))
     return dst_k, dst_v
 
 
@@ -600,3 +605,59 @@ class BoundSegmentedAttention:
         if code != 0:
             _lib.check(code)
         return out
+
+
+class BoundPack:
+    """A pre-validated launch of :func:`pack_flat_segments_kv` (same copy
+    items, source and destination shapes, dtypes, device and stream) repeated
+    for new source and destination tensors: only their pointers pass.
+    ``__call__`` returns False, copying nothing, when the tensors or the
+    stream do not match (or a HIP graph is being captured)."""
+
+    __slots__ = ("_fn", "_args", "_meta", "_dev", "_stream", "_ss", "_ds", "_sdt", "_ddt")
+
+    def __init__(self, record, *, src_k, src_v, dst_k, dst_v):
+        self._fn, args, self._meta = record  # meta: the copy items the recorded pointers refer to
+        self._args = list(args)
+        self._dev = dst_k.get_device()
+        self._stream = args[-1]
+        self._ss, self._ds = src_k.shape, dst_k.shape
+        self._sdt, self._ddt = (src_k.dtype, src_v.dtype), (dst_k.dtype, dst_v.dtype)
+
+    @classmethod
+    def bind(cls, src_shape=None, **kwargs):
+        """Calls :func:`pack_flat_segments_kv` with ``kwargs``; returns the
+        bound copy, or None when nothing was launched (no items) or a HIP
+        graph is being captured.  ``src_shape``: the shape later calls pass
+        their sources in, when not ``kwargs["src_k"]``'s (a contiguous
+        ``[B, H, n, D]`` whose flat view was packed)."""
+        rec = []
+        pack_flat_segments_kv(**kwargs, _bind=rec)
+        if not rec or torch.cuda.is_current_stream_capturing():
+            return None
+        bound = cls(rec[0], src_k=kwargs["src_k"], src_v=kwargs["src_v"], dst_k=kwargs["dst_k"],
+                    dst_v=kwargs["dst_v"])
+        if src_shape is not None:
+            bound._ss = torch.Size(src_shape)
+        return bound
+
+    def __call__(self, src_k, src_v, dst_k, dst_v) -> bool:
+        ss, ds, dev = self._ss, self._ds, self._dev
+        if (src_k.shape != ss or src_v.shape != ss or dst_k.shape != ds or dst_v.shape != ds
+                or (src_k.dtype, src_v.dtype) != self._sdt or (dst_k.dtype, dst_v.dtype) != self._ddt
+                or src_k.get_device() != dev or src_v.get_device() != dev or dst_k.get_device() != dev
+                or dst_v.get_device() != dev or not src_k.is_contiguous() or not src_v.is_contiguous()
+                or not dst_k.is_contiguous() or not dst_v.is_contiguous()):
+            return False
+        stream = torch._C._cuda_getCurrentRawStream(dev)
+        if stream != self._stream or torch.cuda.is_current_stream_capturing():
+            return False
+        a = self._args
+        a[0] = src_k.data_ptr()
+        a[1] = src_v.data_ptr()
+        a[2] = dst_k.data_ptr()
+        a[3] = dst_v.data_ptr()
+        code = self._fn(*a)
+        if code != 0:
+            _lib.check(code)
+        return True

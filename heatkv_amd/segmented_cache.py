@@ -35,6 +35,7 @@ import torch
 
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
+    BoundPack,
     BoundSegmentedAttention,
     attention_fuses_append,
     attention_queries_per_item,
@@ -155,8 +156,12 @@ class _StepReplay:
             (sk, dk), (sv, dv) = self.buf_shapes
             cache.dense_buf = (torch.empty(sk, dtype=dk, device=k.device), torch.empty(sv, dtype=dv, device=v.device))
         buf_k, buf_v = cache.dense_buf
-        B, H, cap = buf_k.shape[0], buf_k.shape[1], buf_k.shape[2]
-        out = self.attn(q, k, v, buf_k.view(B, H * cap, buf_k.shape[3]), buf_v.view(B, H * cap, buf_v.shape[3]))
+        views = cache._dense_views
+        if views is None:
+            B, H, cap = buf_k.shape[0], buf_k.shape[1], buf_k.shape[2]
+            views = cache._dense_views = (buf_k.view(B, H * cap, buf_k.shape[3]),
+                                          buf_v.view(B, H * cap, buf_v.shape[3]))
+        out = self.attn(q, k, v, views[0], views[1])
         if out is None:
             return None
         if self.final:
@@ -166,6 +171,7 @@ class _StepReplay:
         if self.activate is not None:
             cache._activate_from_dense(buf_k, buf_v, self.activate)
             cache.dense_buf = None
+            cache._dense_views = None
         return out
 
 
@@ -182,6 +188,7 @@ class SegmentedLayerCache:
         self._dense_current_plans: Dict[tuple, Tuple[CopyPlan, CopyPlan]] = {}
         # steps recorded by an earlier generation, by scale
         self._replays: Dict[int, _StepReplay] = {}
+        self._packs: Dict[tuple, BoundPack] = {}  # bound slab copies, by copy tag
         self._knobs: Optional[tuple] = None
         self.reset()
 
@@ -199,6 +206,7 @@ class SegmentedLayerCache:
         # the dense prefix kept in place: (K, V) [B, H, rows, D] sized for every
         # dense scale, each step's rows written by its attention launch
         self.dense_buf: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+        self._dense_views = None  # dense_buf seen as slabs [B, H*rows, D] (replayed steps)
 
     def _ensure_slab(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> None:
         """Slab K/V ``[B, capacity, D]`` (:1092-1144); contents of unowned rows are undefined."""
@@ -217,13 +225,24 @@ class SegmentedLayerCache:
         B, H, n, D = src_k.shape
         if n != plan.sequence_len:
             raise RuntimeError("static precomputed copy run sequence length mismatch")
-        dst_starts, src_starts, lengths = self.schedule.device_plan(plan, src_k.device, tag)
         prof.stat_add("static_copy_calls")
         prof.record_kv_copy("static_copy", slots=plan.slots, k_tensor=src_k, v_tensor=src_v)
-        pack_flat_segments_kv(dst_k=self.cached_k, dst_v=self.cached_v,
-                              src_k=src_k.reshape(B, H * n, D), src_v=src_v.reshape(B, H * n, D),
-                              dst_starts=dst_starts, src_starts=src_starts, lengths=lengths,
-                              max_length=plan.max_length)
+        if not prof._enabled:
+            bound = self._packs.get(tag)
+            if bound is not None and bound(src_k, src_v, self.cached_k, self.cached_v):
+                return
+        dst_starts, src_starts, lengths = self.schedule.device_plan(plan, src_k.device, tag)
+        kw = dict(dst_k=self.cached_k, dst_v=self.cached_v,
+                  src_k=src_k.reshape(B, H * n, D), src_v=src_v.reshape(B, H * n, D),
+                  dst_starts=dst_starts, src_starts=src_starts, lengths=lengths, max_length=plan.max_length)
+        if src_k.is_cuda and not prof._enabled and not _capturing():
+            # later copies of this plan go through the bound launch (same 4-D
+            # source shape: the flat view has the source's pointer)
+            bound = BoundPack.bind(src_shape=src_k.shape, **kw)
+            if bound is not None:
+                self._packs[tag] = bound
+        else:
+            pack_flat_segments_kv(**kw)
 
     def _activate_from_dense(self, dense_k, dense_v, target: int) -> None:
         """Pack the dense cache into a new slab for ``target`` (:1639-1711)."""
@@ -352,6 +371,7 @@ class SegmentedLayerCache:
                 with prof.phase("compact"):
                     self._activate_from_dense(buf_k, buf_v, activate)
                 self.dense_buf = None
+                self._dense_views = None
         if bound is not None:
             self._replays[scale_ind] = _StepReplay(
                 record, "dense", bound, old_len, old_len + L, final,
@@ -448,7 +468,7 @@ class SegmentedLayerCache:
         (``qkv_produce(..., k_split_rows=True)``); every step of a generation
         passes the same value, and the cache's K rows keep that format."""
         record = None
-        if not prof.phase_profile_enabled():
+        if not prof._enabled:
             if self.logical_len == 0:
                 knobs = tuple(os.environ.get(n) for n in _STEP_KNOBS)
                 if knobs != self._knobs:
