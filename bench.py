@@ -132,11 +132,11 @@ def attention_call(wl, device):
 
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
-    from heatkv_amd import attention_queries_per_item
+    from heatkv_amd import attention_item_shape
 
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
     plan = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len,
-                                         queries_per_item=attention_queries_per_item(q.dtype, ck.dtype, cv.dtype))
+                                         item_shape=attention_item_shape(q.dtype, ck.dtype, cv.dtype, device=device))
             if work_plans_enabled(device) else None)
     return dict(q=q, persisted_k=slab_k, persisted_v=slab_v, segment_starts=st, segment_ends=en,
                 segment_counts=ct, current_k=ck, current_v=cv, softmax_scale=wl.softmax_scale,
@@ -489,7 +489,7 @@ def time_real_model(device, steps=50, warmup=20):
 
     from heatkv_amd import workloads as W
 
-    from heatkv_amd import attention_queries_per_item
+    from heatkv_amd import attention_item_shape
     from heatkv_amd.segmented_cache import work_plans_enabled
 
     wl = W.config(2)
@@ -499,8 +499,8 @@ def time_real_model(device, steps=50, warmup=20):
     kw["current_k"] = F.normalize(kw["current_k"].float(), dim=-1)
     kw["persisted_k"] = F.normalize(kw["persisted_k"].float().nan_to_num(0.0), dim=-1)
     kw["softmax_scale"] = 1.0
-    qpi = attention_queries_per_item(torch.float32, torch.float32, kw["current_v"].dtype)
-    kw["work_plan"] = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len, queries_per_item=qpi)
+    shape = attention_item_shape(torch.float32, torch.float32, kw["current_v"].dtype, device=device)
+    kw["work_plan"] = (wl.schedule.device_work_plan(wl.target, device, wl.batch, wl.cur_len, item_shape=shape)
                        if work_plans_enabled(device) else None)
     # fp32 K split on every call (the operator's own split, two extra launches)
     ms_split = time_attention_median(kw, device, steps, warmup)

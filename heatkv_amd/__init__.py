@@ -7,6 +7,7 @@ descriptors) is computed on the host like the reference's.
 """
 
 from .real_pruning_fused_attention import (  # noqa: F401
+    attention_item_shape,
     attention_queries_per_item,
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
@@ -37,4 +38,4 @@ from .phase_profile import (  # noqa: F401
     snapshot_real_pruning_fast_phase_profile,
 )
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"

@@ -516,7 +516,8 @@ int32_t hkv_segmented_attention_item_shape(int32_t q_dtype, int32_t k_dtype, int
   if (slots != nullptr) {
     const int32_t s = hkv::split_slots(device);
     if (s <= 0) return fail(HKV_ERR_DEVICE, "cannot query the CU count of device %d", device);
-    *slots = q == 128 ? s : s / 2;  // 2 workgroups per CU, or 1 for the 256-query kernel
+    // split_slots counts 2 workgroups per CU
+    *slots = hkv::attention_workgroups_per_cu(a) == 2 ? s : s / 2;
   }
   ok();
   return q;

@@ -104,6 +104,8 @@ int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
 // at the default dot modes; 256-query items, one workgroup per CU.
 bool attention_split_supported(const AttnArgs& a);
 int32_t attention_item_queries(const AttnArgs& a);
+// Resident workgroups per CU of the attention kernel that runs for a (1 or 2).
+int32_t attention_workgroups_per_cu(const AttnArgs& a);
 hipError_t launch_split_rows(const float* src, void* dst, int64_t rows, hipStream_t stream);
 
 constexpr int kMaxSegments = 256;

@@ -36,6 +36,16 @@ bool force_staged() {
 }
 }  // namespace
 
+int32_t attention_workgroups_per_cu(const AttnArgs& a) {
+  if (a.k_dtype == kSplitRows) return 1;
+  if (!force_staged() && attention_direct_supported(a)) return 2;
+  // the staged kernel's split modes (3-piece q/k, fp32 value mode, fp32 V)
+  // hold more pieces per wave: one workgroup per CU
+  const bool split = (a.q_dtype == kF32 && a.qk_dot_mode == kDotFp32) || a.value_dot_mode == kDotFp32 ||
+                     a.v_dtype == kF32;
+  return split ? 1 : 2;
+}
+
 hipError_t launch_segmented_attention(const AttnArgs& a, hipStream_t stream) {
   if (a.heads > attn::kMaxHeads) return hipErrorInvalidValue;
   attn::Scalars s;

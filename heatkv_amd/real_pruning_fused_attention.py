@@ -31,6 +31,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+import ctypes
 import os
 from typing import Optional
 
@@ -89,9 +90,11 @@ def segmented_attention_plan(segment_starts, segment_ends, segment_counts, *, ba
     and the batch size and length as ``hkv_plan_shape``, and the operator
     checks both (a copy made with ``clone()`` / ``to()`` loses them and is
     refused).  Built on the host by
-    ``hkv_segmented_attention_plan``; ``slots`` defaults to the device's
-    resident attention workgroups for that kernel.  No counterpart in the
-    reference, whose Triton grid walks the tables directly."""
+    ``hkv_segmented_attention_plan``; ``slots`` is the kernel's resident
+    workgroups (:func:`attention_item_shape`), by default 2 per CU of the
+    device for 128-query items (the 16-bit kernel) and 1 per CU for 256.
+    No counterpart in the reference, whose Triton grid walks the tables
+    directly."""
     import numpy as np
 
     def host(t):
@@ -156,6 +159,48 @@ def _check_split_rows_k(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int
                          "float32 K)")
 
 
+def _kernel_qk_dtypes(q_dtype, k_dtype, qk_mode: int, k_split_rows: bool):
+    """q/k dtypes the kernels see: q and k of different dtypes (not split K
+    rows) run widened to fp32 under the tf32 and fp32 QK modes
+    (_promote_mixed_qk; the default mode refuses them)."""
+    if q_dtype != k_dtype and not k_split_rows and qk_mode != 0:
+        return torch.float32, torch.float32
+    return q_dtype, k_dtype
+
+
+_ITEM_SHAPES: dict = {}
+
+
+def attention_item_shape(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool = False, device=None):
+    """``(queries_per_item, slots)`` of the kernel that
+    :func:`fused_real_pruning_flat_segmented_attention` runs for these dtypes
+    at the current dot-mode knobs on ``device`` (the current CUDA device when
+    None), as the library reports them (``hkv_segmented_attention_item_shape``):
+    the ``queries_per_item`` and ``slots`` of :func:`segmented_attention_plan`.
+    Items are 128 queries, or 256 for the 8-wave form of the split-row
+    kernel; slots are the resident workgroups of that kernel (2 per CU for
+    the 16-bit kernel and the staged kernel's plain modes, 1 per CU for the
+    split-row kernel and the staged kernel's split modes).  slots is None
+    for a device that is not a GPU (no kernel runs there)."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if dev.type != "cuda":
+        return (attention_queries_per_item(q_dtype, k_dtype, v_dtype, k_split_rows=k_split_rows), None)
+    qk_mode, value_mode = _fused_qk_dot_mode_id(), _fused_value_dot_mode_id()
+    qd, kd = _kernel_qk_dtypes(q_dtype, k_dtype, qk_mode, k_split_rows)
+    split = k_split_rows or _split_rows_path(qd, kd, v_dtype, qk_mode, value_mode)
+    codes = (_lib.dtype_code(qd), _lib.DTYPE_SPLIT_ROWS if split else _lib.dtype_code(kd), _lib.dtype_code(v_dtype))
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (codes, qk_mode, value_mode, idx)
+    hit = _ITEM_SHAPES.get(key)
+    if hit is None:
+        slots = ctypes.c_int32(0)
+        n = int(_lib.load().hkv_segmented_attention_item_shape(*codes, 1, qk_mode, value_mode, idx,
+                                                               ctypes.byref(slots)))
+        _lib.check(min(n, 0))
+        hit = _ITEM_SHAPES[key] = (n, int(slots.value))
+    return hit
+
+
 def attention_queries_per_item(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool = False) -> int:
     """Queries per work item of the kernel that :func:`fused_real_pruning_flat_segmented_attention`
     runs for these dtypes at the current dot-mode knobs (the ``queries_per_item``
@@ -163,10 +208,11 @@ def attention_queries_per_item(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool 
     (``hkv_segmented_attention_item_shape``): 128, or 256 for the 8-wave form
     of the split-row kernel."""
     qk_mode, value_mode = _fused_qk_dot_mode_id(), _fused_value_dot_mode_id()
-    if not (k_split_rows or _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode, value_mode)):
+    qd, kd = _kernel_qk_dtypes(q_dtype, k_dtype, qk_mode, k_split_rows)
+    if not (k_split_rows or _split_rows_path(qd, kd, v_dtype, qk_mode, value_mode)):
         return 128
     n = int(_lib.load().hkv_segmented_attention_item_shape(
-        _lib.dtype_code(q_dtype), _lib.DTYPE_SPLIT_ROWS, _lib.dtype_code(v_dtype), 1, qk_mode, value_mode, 0, None))
+        _lib.dtype_code(qd), _lib.DTYPE_SPLIT_ROWS, _lib.dtype_code(v_dtype), 1, qk_mode, value_mode, 0, None))
     _lib.check(min(n, 0))
     return n
 
@@ -174,10 +220,16 @@ def attention_queries_per_item(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool 
 def attention_fuses_append(q_dtype, k_dtype, v_dtype, *, k_split_rows: bool = False) -> bool:
     """Whether :func:`fused_real_pruning_flat_segmented_attention` takes
     ``append_offsets`` for these dtypes at the current dot-mode knobs: every
-    path but the one that splits fp32 K itself (its slab K is a split copy);
+    path but the one that splits fp32 K itself (its slab K is a split copy)
+    and q/k of different dtypes with 16-bit k (widened to fp32 for the call);
     K already in split rows (``k_split_rows``) takes it."""
-    return k_split_rows or not _split_rows_path(q_dtype, k_dtype, v_dtype, _fused_qk_dot_mode_id(),
-                                                _fused_value_dot_mode_id())
+    if k_split_rows:
+        return True
+    qk_mode, value_mode = _fused_qk_dot_mode_id(), _fused_value_dot_mode_id()
+    qd, kd = _kernel_qk_dtypes(q_dtype, k_dtype, qk_mode, False)
+    if kd != k_dtype:
+        return False
+    return not _split_rows_path(qd, kd, v_dtype, qk_mode, value_mode)
 
 
 def _split_rows(t: torch.Tensor, stream) -> torch.Tensor:
@@ -549,8 +601,6 @@ class BoundSegmentedAttention:
                  "_qs", "_ps", "_qdt", "_kdt", "_vdt", "_skdt", "_svdt")
 
     def __init__(self, record, *, q, current_k, current_v, persisted_k, persisted_v):
-        import ctypes
-
         fn, a, out_shape, out_dtype, keep = record
         lib = _lib.load()
         size = int(lib.hkv_segmented_attention_bound_bytes())

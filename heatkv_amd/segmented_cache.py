@@ -38,7 +38,7 @@ from .real_pruning_fused_attention import (
     BoundPack,
     BoundSegmentedAttention,
     attention_fuses_append,
-    attention_queries_per_item,
+    attention_item_shape,
     concat_kv,
     fused_real_pruning_flat_segmented_attention,
     pack_flat_segments_kv,
@@ -303,20 +303,22 @@ class SegmentedLayerCache:
         act = next((t for t in range(1, self.num_scales) if has_removed(self.removed(t))), self.num_scales - 1)
         return int(self.schedule.scale_ranges[act - 1][1]) if act >= 1 else 0
 
-    def _in_place_tables(self, heads: int, cap: int, old_len: int, device, batch: int, L: int, qpi: int,
+    def _in_place_tables(self, heads: int, cap: int, old_len: int, device, batch: int, L: int, shape: tuple,
                          store: bool):
         """Tables presenting rows ``[0, old_len)`` of each head of the in-place
         dense prefix ``[B, H, cap, D]`` as a slab ``[B, H*cap, D]``, their work
         plan, and the append offsets ``h*cap + old_len`` of this step's rows
-        (None when nothing is stored), made once."""
-        key = ("in_place", heads, cap, old_len, str(device), batch, L, qpi, store)
+        (None when nothing is stored), made once.  ``shape``: the kernel's
+        ``(queries_per_item, slots)`` (attention_item_shape)."""
+        key = ("in_place", heads, cap, old_len, str(device), batch, L, shape, store)
         hit = self._tables_by_len.get(key)
         if hit is None:
             starts = (torch.arange(heads, dtype=torch.int32) * cap).reshape(heads, 1)
             ends = starts + old_len
             counts = torch.ones((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
-                                             capacity=heads * cap, device=device, queries_per_item=qpi)
+                                             capacity=heads * cap, device=device, queries_per_item=shape[0],
+                                             slots=shape[1])
                     if work_plans_enabled(device) and not _capturing() else None)
             offs = (starts.reshape(heads) + old_len).to(device) if store else None
             hit = (starts.to(device), ends.to(device), counts.to(device), plan, offs)
@@ -347,8 +349,8 @@ class SegmentedLayerCache:
         store = not final
         if store and old_len + L > cap:
             raise RuntimeError("dense prefix longer than its in-place buffer")
-        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows)
-        st, en, ct, plan, offs = self._in_place_tables(H, cap, old_len, q.device, B, L, qpi, store)
+        shape = attention_item_shape(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows, device=q.device)
+        st, en, ct, plan, offs = self._in_place_tables(H, cap, old_len, q.device, B, L, shape, store)
         kw = dict(q=q, persisted_k=buf_k.reshape(B, H * cap, buf_k.shape[3]),
                   persisted_v=buf_v.reshape(B, H * cap, buf_v.shape[3]), segment_starts=st, segment_ends=en,
                   segment_counts=ct, current_k=k, current_v=v, softmax_scale=scale, softmax_mode=mode,
@@ -380,33 +382,34 @@ class SegmentedLayerCache:
 
     # ------------------------------------------------------------------ attention
 
-    def _dense_tables(self, heads: int, T: int, device, batch: int, L: int, qpi: int = 128):
+    def _dense_tables(self, heads: int, T: int, device, batch: int, L: int, shape: tuple):
         """Offset tables that present a dense cache ``[B, H, T, D]`` as a slab
         ``[B, H*T, D]``, and their work plan for ``batch`` x ``L`` queries
-        (``qpi``: the kernel's queries per item)."""
-        key = (heads, T, str(device), batch, L, qpi)
+        (``shape``: the kernel's ``(queries_per_item, slots)``)."""
+        key = (heads, T, str(device), batch, L, shape)
         hit = self._tables_by_len.get(key)
         if hit is None:
             starts = (torch.arange(heads, dtype=torch.int32) * T).reshape(heads, 1)
             ends = starts + T
             counts = torch.ones((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(starts, ends, counts, batch_size=batch, current_len=L,
-                                             capacity=heads * T, device=device, queries_per_item=qpi)
+                                             capacity=heads * T, device=device, queries_per_item=shape[0],
+                                             slots=shape[1])
                     if work_plans_enabled(device) and not _capturing() else None)
             hit = (starts.to(device), ends.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
         return hit
 
-    def _empty_tables(self, heads: int, device, batch: int, L: int, qpi: int = 128):
+    def _empty_tables(self, heads: int, device, batch: int, L: int, shape: tuple):
         """Tables with no segment (attention over the current scale only) and
         their work plan, made once."""
-        key = ("empty", heads, str(device), batch, L, qpi)
+        key = ("empty", heads, str(device), batch, L, shape)
         hit = self._tables_by_len.get(key)
         if hit is None:
             empty = torch.zeros((heads, 0), dtype=torch.int32)
             counts = torch.zeros((heads,), dtype=torch.int32)
             plan = (segmented_attention_plan(empty, empty, counts, batch_size=batch, current_len=L, capacity=0,
-                                             device=device, queries_per_item=qpi)
+                                             device=device, queries_per_item=shape[0], slots=shape[1])
                     if work_plans_enabled(device) and not _capturing() else None)
             hit = (empty.to(device), empty.to(device), counts.to(device), plan)
             self._tables_by_len[key] = hit
@@ -414,13 +417,13 @@ class SegmentedLayerCache:
 
     def _attend_dense(self, q, k, v, scale, mode, out_dtype=None):
         B, H, L, D = q.shape
-        qpi = attention_queries_per_item(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows)
+        shape = attention_item_shape(q.dtype, k.dtype, v.dtype, k_split_rows=self.k_split_rows, device=q.device)
         if self.cached_k is None or self.logical_len == 0:
-            tables = self._empty_tables(H, q.device, B, L, qpi)
+            tables = self._empty_tables(H, q.device, B, L, shape)
             slab_k = slab_v = None
         else:
             T = self.cached_k.shape[2]
-            tables = self._dense_tables(H, T, q.device, B, L, qpi)
+            tables = self._dense_tables(H, T, q.device, B, L, shape)
             slab_k = self.cached_k.reshape(B, H * T, D)
             slab_v = self.cached_v.reshape(B, H * T, D)
         return fused_real_pruning_flat_segmented_attention(
@@ -538,9 +541,9 @@ class SegmentedLayerCache:
                 starts, ends, counts = self.schedule.device_tables(scale_ind, q.device)
                 plan = (self.schedule.device_work_plan(scale_ind, q.device, int(q.shape[0]), int(q.shape[2]),
                                                        build=not _capturing(),
-                                                       queries_per_item=attention_queries_per_item(
+                                                       item_shape=attention_item_shape(
                                                            q.dtype, k.dtype, v.dtype,
-                                                           k_split_rows=self.k_split_rows))
+                                                           k_split_rows=self.k_split_rows, device=q.device))
                         if work_plans_enabled(q.device) else None)
                 offsets = None if final or appended else self._fused_append_offsets(scale_ind, q, k, v)
                 fused = offsets is not None

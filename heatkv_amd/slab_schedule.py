@@ -134,21 +134,23 @@ class SlabSchedule:
         return hit
 
     def device_work_plan(self, target: int, device, batch: int, cur_len: int, *, build: bool = True,
-                         queries_per_item: int = 128) -> Optional[torch.Tensor]:
+                         item_shape: Tuple[int, Optional[int]] = (128, None)) -> Optional[torch.Tensor]:
         """Attention work plan of ``target``'s tables for ``batch`` rows of
         ``cur_len`` queries on ``device`` (segmented_attention_plan) for a
-        kernel of ``queries_per_item``-query items, built on the host and
-        moved once, cached.  With ``build=False`` only a plan already made is
-        returned (None otherwise)."""
+        kernel's ``item_shape`` (``(queries_per_item, slots)``, as
+        attention_item_shape reports it; slots None: the device's default),
+        built on the host and moved once, cached.  With ``build=False`` only
+        a plan already made is returned (None otherwise)."""
         from .real_pruning_fused_attention import segmented_attention_plan
 
-        key = ("work_plan", str(device), int(target), int(batch), int(cur_len), int(queries_per_item))
+        qpi, slots = item_shape
+        key = ("work_plan", str(device), int(target), int(batch), int(cur_len), int(qpi), slots)
         hit = self._device_cache.get(key)
         if hit is None and build:
             st, en, ct = self.tables[int(target)]
             hit = segmented_attention_plan(st, en, ct, batch_size=batch, current_len=cur_len,
                                            capacity=self.capacity, device=device,
-                                           queries_per_item=queries_per_item)
+                                           queries_per_item=qpi, slots=slots)
             self._device_cache[key] = hit
         return hit
 

@@ -247,10 +247,13 @@ int32_t hkv_segmented_attention_plan(const int32_t* seg_starts, const int32_t* s
 /*
  * Item shape of hkv_segmented_attention for these dtypes and dot modes:
  * returns the queries per work item (128, or 256 for split K rows), and
- * writes the device's resident attention workgroups for that kernel to
- * *slots when slots is not NULL (the `queries_per_item` and `slots` of
- * hkv_segmented_attention_plan); a negative HKV_ERR_* code when the device
- * cannot be queried.  No counterpart in the reference.
+ * writes the device's resident attention workgroups for the kernel that runs
+ * (2 per CU for the 16-bit kernel and the staged kernel's plain modes, 1 per
+ * CU for split K rows and for the staged kernel's fp32 QK dot mode on fp32 q,
+ * fp32 value dot mode and fp32 V) to *slots when slots is not NULL (the
+ * `queries_per_item` and `slots` of hkv_segmented_attention_plan); a negative
+ * HKV_ERR_* code when the device cannot be queried.  No counterpart in the
+ * reference.
  */
 int32_t hkv_segmented_attention_item_shape(int32_t q_dtype, int32_t k_dtype, int32_t v_dtype, int32_t heads,
                                            int32_t qk_dot_mode, int32_t value_dot_mode, int32_t device,

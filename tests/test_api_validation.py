@@ -138,3 +138,30 @@ def test_mixed_qk_promotion_rules():
     qb = q.to(torch.bfloat16)
     q3, sk3, k3 = _promote_mixed_qk(qb, sk.float(), k.float(), 2, torch.zeros(2, dtype=torch.int32))
     assert q3.dtype == torch.float32 and torch.equal(q3, qb.float()) and k3.dtype == torch.float32
+
+
+def test_item_shape_helpers_follow_promotion(monkeypatch):
+    """attention_queries_per_item and attention_fuses_append answer for the
+    kernel the operator runs after widening mixed q/k to fp32: under tf32,
+    bf16 q with fp32 k and 16-bit v is the split-row kernel's call (256-query
+    items, no fused append), and fp32 q with 16-bit k widens k, which refuses
+    the append."""
+    from heatkv_amd.real_pruning_fused_attention import attention_fuses_append, attention_queries_per_item
+
+    f32, bf16 = torch.float32, torch.bfloat16
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "tf32")
+    assert attention_queries_per_item(f32, f32, bf16) == 256
+    assert attention_queries_per_item(bf16, f32, bf16) == 256
+    assert attention_queries_per_item(f32, bf16, bf16) == 256
+    assert attention_queries_per_item(bf16, bf16, bf16) == 128
+    assert not attention_fuses_append(bf16, f32, bf16)
+    assert not attention_fuses_append(f32, bf16, bf16)
+    assert attention_fuses_append(bf16, bf16, bf16)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "fp32")
+    # staged fp32 kernel: 128-query items; fp32 k takes the append, widened bf16 k does not
+    assert attention_queries_per_item(bf16, f32, bf16) == 128
+    assert attention_fuses_append(bf16, f32, bf16)
+    assert not attention_fuses_append(f32, bf16, bf16)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16")
+    # the default mode refuses mixed q/k; the helpers answer for the dtypes as given
+    assert attention_queries_per_item(bf16, f32, bf16) == 128

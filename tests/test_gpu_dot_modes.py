@@ -158,3 +158,52 @@ def test_mixed_qk_dtypes_default_mode_raises(device, monkeypatch):
             q=q.float().to(device), persisted_k=sk.to(device), persisted_v=sv.to(device),
             segment_starts=st.to(device), segment_ends=en.to(device), segment_counts=ct.to(device),
             current_k=ck.to(device), current_v=cv.to(device), softmax_scale=0.125)
+
+
+@pytest.mark.parametrize("qk_mode,value_mode,qdt,kdt,vdt,per_cu,qpi", [
+    ("bf16", "bf16", torch.bfloat16, torch.bfloat16, torch.bfloat16, 2, 128),  # 16-bit kernel
+    ("tf32", "bf16", torch.float16, torch.float16, torch.float16, 2, 128),  # 16-bit kernel, exact products
+    ("fp32", "bf16", torch.float32, torch.float32, torch.bfloat16, 1, 128),  # staged, 3-piece q/k
+    ("bf16", "fp32", torch.bfloat16, torch.bfloat16, torch.bfloat16, 1, 128),  # staged, fp32 P V
+    ("bf16", "bf16", torch.bfloat16, torch.bfloat16, torch.float32, 1, 128),  # staged, fp32 V
+    ("tf32", "bf16", torch.bfloat16, torch.float32, torch.bfloat16, 1, 256),  # widened q: split-row kernel
+])
+def test_item_shape_slots_and_planned_calls(qk_mode, value_mode, qdt, kdt, vdt, per_cu, qpi, device, monkeypatch):
+    """attention_item_shape reports the resident workgroups of the kernel
+    that runs (1 per CU for the staged kernel's split modes and the split-row
+    kernel, 2 for the others), and a plan built with them runs that kernel as
+    accurately as the unplanned call: max-abs errors against the fp64 oracle
+    within twice the unplanned call's (a cut item restarts its running max,
+    which moves the rounding of P in the 16-bit value modes)."""
+    from heatkv_amd import attention_item_shape, segmented_attention_plan
+
+    monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", qk_mode)
+    monkeypatch.setenv("REAL_PRUNING_FUSED_VALUE_DOT_MODE", value_mode)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    shape = attention_item_shape(qdt, kdt, vdt, device=device)
+    print(f"[dot] item shape qk={qk_mode} value={value_mode} {qdt}/{kdt}/{vdt}: {shape}, {cus} CUs", flush=True)
+    assert shape == (qpi, per_cu * cus)
+    B, L, cap = 2, 700, 3000
+    q, sk, sv, (st, en, ct), ck, cv = _case(87, torch.float32, torch.float32, B=B, H=3, L=L, cap=cap, S=12)
+    q, sk, ck, sv, cv = q.to(qdt), sk.to(kdt), ck.to(kdt), sv.to(vdt), cv.to(vdt)
+    plan = segmented_attention_plan(st, en, ct, batch_size=B, current_len=L, capacity=cap, device=device,
+                                    queries_per_item=shape[0], slots=shape[1])
+    ref_out, ref_lse = oattn.flat_segmented_attention(
+        to_np(q).astype(np.float64), to_np(sk).astype(np.float64), to_np(sv).astype(np.float64),
+        st.numpy(), en.numpy(), ct.numpy(), to_np(ck).astype(np.float64), to_np(cv).astype(np.float64),
+        0.125, dtype=np.float64, workers=16)
+    errs = []
+    for wp in (None, plan):
+        out, lse = fused_real_pruning_flat_segmented_attention(
+            q=q.to(device), persisted_k=sk.to(device), persisted_v=sv.to(device), segment_starts=st.to(device),
+            segment_ends=en.to(device), segment_counts=ct.to(device), current_k=ck.to(device),
+            current_v=cv.to(device), softmax_scale=0.125, return_lse=True, out_dtype=torch.float32,
+            work_plan=wp)
+        torch.cuda.synchronize(device)
+        o = out.double().cpu().numpy()
+        l = lse.double().cpu().numpy()
+        assert np.isfinite(o).all() and np.isfinite(l).all()
+        errs.append((float(np.abs(o - ref_out).max()), float(np.abs(l - ref_lse).max())))
+    print(f"[dot] max-abs (out, lse): unplanned {errs[0]}, planned {errs[1]}", flush=True)
+    assert errs[1][0] <= 2 * errs[0][0] + 1e-6
+    assert errs[1][1] <= 2 * errs[0][1] + 1e-6
