@@ -521,7 +521,7 @@ def time_real_model(device, steps=50, warmup=20):
     kw["work_plan"] = plan16
     ms16 = time_attention_median(kw, device, steps, warmup)
     flops = wl.attention_flops()
-    kernel = f"split-row kernel ({qpi}-query items), K held as split rows as the producer writes it"
+    kernel = f"split-row kernel ({shape[0]}-query items), K held as split rows as the producer writes it"
     return {"what": f"2b_final_1024 with fp32 q (x30) / k (unit), bf16 v, scale 1 ({kernel})",
             "ms_per_step": round(ms, 4), "tflops_nominal": round(flops / (ms * 1e-3) / 1e12, 1),
             "pct_of_bf16_peak_nominal": round(100.0 * flops / (ms * 1e-3) / PEAK_BF16_FLOPS, 2),

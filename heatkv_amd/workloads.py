@@ -213,6 +213,22 @@ def sweep_keep_policies(layers: int = 32, heads: int = 16, sides=SIDES_1M, budge
     return out
 
 
+def sweep_step(layer: int, target: int, *, layers: int = 32, batch: int = 2, heads: int = 16,
+               sides=SIDES_1M, seed: Optional[int] = None, dtype=torch.bfloat16) -> FinalStepWorkload:
+    """Step ``target`` of layer ``layer`` of the generation sweep as a
+    workload: the sweep's keep policy and slab schedule (built for the whole
+    generation, so its tables and capacity are the ones the sweep's cache
+    uses at that step) with fresh N(0, 1) inputs of the scales up to
+    ``target`` (seed 3000 + 16 layer + target by default)."""
+    keep = sweep_keep_policies(layers=layers, heads=heads, sides=sides)[layer]
+    sched = schedule_from_keep(keep, sides)
+    seed = 3000 + 16 * layer + target if seed is None else int(seed)
+    gen = torch.Generator().manual_seed(seed)
+    q, pk, pv, ck, cv = _draw_inputs(gen, batch, heads, tuple(sides[:target + 1]), dtype)
+    return FinalStepWorkload(f"sweep_layer{layer}_step{target}", batch, heads, tuple(sides[:target + 1]), seed,
+                             0.1, keep, q, pk, pv, ck, cv, sched, 1.0 / math.sqrt(HEAD_DIM))
+
+
 def build_slab(wl: FinalStepWorkload, device, *, fill: float = float("nan")):
     """Slab K/V of a final-step workload, filled by the HIP pack kernel.
 

@@ -12,9 +12,11 @@ the reference CPU path restated) with the contract tolerances: out max-abs
 Workloads: the 2B final step (B=2, H=16, budget 0.1), the 8B-class final step
 (B=8, H=32) at budgets 0.05, 0.1, 0.2 and 1.0 (every prior token kept), and
 the skewed-ragged step (B=16, H=16, retained lengths log-uniform in
-[0, 6425]) -- every (b, h) of each; and the 2B final step at the model's
-precision (fp32 q of norm 30, unit fp32 k, bf16 v, scale 1: the staged
-kernel) against the oracle in fp64.
+[0, 6425]) -- every (b, h) of each; the generation sweep's mid-scale steps
+(1024 and 2304 queries: fewer than two rounds of items, so the plan cuts
+most of them) with the sweep's own tables and work plan; and the 2B final
+step at the model's precision (fp32 q of norm 30, unit fp32 k, bf16 v,
+scale 1: the staged kernel) against the oracle in fp64.
 """
 
 from __future__ import annotations
@@ -42,11 +44,11 @@ def model_precision(q, slab_k, ck):
             F.normalize(ck.float(), dim=-1))
 
 
-def abi_attention(wl, device, *, workspace=True, planned=False, model=False, split_rows=False):
+def abi_attention(wl, device, *, workspace=True, planned=False, model=False, split_rows=False, plan=None):
     """One call of hkv_segmented_attention on ``wl`` into NaN-prefilled out / lse
     (``planned``: with the host work plan of its tables; ``model``: fp32 q/k at
     the model's precision, scale 1, see model_precision; ``split_rows``: K
-    passed as split rows, the split-row kernel)."""
+    passed as split rows, the split-row kernel; ``plan``: this work plan)."""
     slab_k, slab_v = W.build_slab(wl, device)
     st, en, ct = wl.schedule.device_tables(wl.target, device)
     q, ck, cv = (t.to(device) for t in (wl.q, wl.cur_k, wl.cur_v))
@@ -58,8 +60,7 @@ def abi_attention(wl, device, *, workspace=True, planned=False, model=False, spl
     out = torch.full((B, L, H * D), float("nan"), dtype=q.dtype, device=device)
     lse = torch.full((B, H, L), float("nan"), dtype=torch.float32, device=device)
     ws = _lib.attention_workspace(device) if workspace else None
-    plan = None
-    if planned:
+    if planned and plan is None:
         hst, hen, hct = wl.tables()
         qpi = 128
         if split_rows:
@@ -164,3 +165,22 @@ def test_every_row_skewed_ragged_planned(device):
 @pytest.mark.parametrize("split_rows", [False, True])
 def test_every_row_2b_final_model_precision(planned, split_rows, device):
     check_every_row(W.config(2), device, planned=planned, model=True, split_rows=split_rows)
+
+
+# The generation sweep's mid-scale steps, with the tables and the work plan
+# its cache uses (SlabSchedule.device_work_plan at attention_item_shape):
+# scale 9 (1024 queries: 256 items for 512 slots, every item cut in two) and
+# scale 11 (2304 queries: 576 items), layers 0 and 31.
+@pytest.mark.parametrize("layer", [0, 31])
+@pytest.mark.parametrize("target", [9, 11])
+def test_every_row_sweep_mid_scale_planned(target, layer, device):
+    from heatkv_amd import attention_item_shape
+
+    wl = W.sweep_step(layer, target)
+    B, H, L, _ = wl.q.shape
+    shape = attention_item_shape(wl.q.dtype, wl.cur_k.dtype, wl.cur_v.dtype, device=device)
+    plan = wl.schedule.device_work_plan(wl.target, device, B, L, item_shape=shape)
+    cuts = int((plan[:, 4].cpu() >= 0).sum())
+    print(f"[full] sweep layer {layer} step {target}: {plan.shape[0]} units, {cuts} cut parts, slots {shape[1]}",
+          flush=True)
+    check_every_row(wl, device, planned=True, plan=plan)
