@@ -103,6 +103,24 @@ _STEP_KNOBS = ("REAL_PRUNING_FUSED_QK_DOT_MODE", "REAL_PRUNING_FUSED_VALUE_DOT_M
                "REAL_PRUNING_FUSED_NUM_STAGES", "HKV_ATTN_SPLIT", "HKV_ATTN_PLAN", "HKV_FUSED_APPEND",
                "HKV_ATTN_SPLIT_ROWS")
 
+# os.environ keeps its values in a dict of encoded keys (CPython on POSIX;
+# os.environ[...] = ... updates it): reading the knobs from it directly takes
+# ~0.5 us per generation and layer instead of ~6 us through os.environ.get.
+_ENV_DATA = getattr(os.environ, "_data", None)
+_STEP_KNOB_KEYS = None
+if isinstance(_ENV_DATA, dict):
+    try:
+        _STEP_KNOB_KEYS = tuple(os.environ.encodekey(n) for n in _STEP_KNOBS)
+    except Exception:  # pragma: no cover - another platform's os.environ
+        _STEP_KNOB_KEYS = None
+
+
+def _step_knobs() -> tuple:
+    """The knobs a replayed step depends on, as the environment has them now."""
+    if _STEP_KNOB_KEYS is not None:
+        return tuple(map(_ENV_DATA.get, _STEP_KNOB_KEYS))
+    return tuple(os.environ.get(n) for n in _STEP_KNOBS)
+
 
 class _StepReplay:
     """One recorded step of a generation (scale, shapes, dtypes and arguments
@@ -473,7 +491,7 @@ class SegmentedLayerCache:
         record = None
         if not prof._enabled:
             if self.logical_len == 0:
-                knobs = tuple(os.environ.get(n) for n in _STEP_KNOBS)
+                knobs = _step_knobs()
                 if knobs != self._knobs:
                     self._replays.clear()
                     self._knobs = knobs
