@@ -38,4 +38,4 @@ from .phase_profile import (  # noqa: F401
     snapshot_real_pruning_fast_phase_profile,
 )
 
-__version__ = "0.2.0"
+__version__ = "0.3.0"

@@ -25,7 +25,7 @@ HKV_ERR_DEVICE = -4
 
 # HKV_VERSION of include/heatkv.h these bindings follow (SIGNATURES below);
 # load() refuses a library built from another version of the header.
-ABI_VERSION = (0 << 16) | (2 << 8) | 0
+ABI_VERSION = (0 << 16) | (3 << 8) | 0
 
 DTYPE_CODES = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
 DTYPE_SPLIT_ROWS = 4  # K only: fp32 rows as bf16 high parts then low parts (hkv_split_rows)
@@ -65,6 +65,12 @@ SIGNATURES = {
          _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
          _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_p],
     ),
+    "hkv_segmented_attention_append2": (
+        _c_i32,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
+         _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_i32, _c_i32,
+         _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p],
+    ),
     "hkv_segmented_attention_noalloc": (
         _c_i32,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
@@ -76,6 +82,12 @@ SIGNATURES = {
         _c_i32,
         [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
          _c_i32, ctypes.c_float, _c_i32, _c_i32, _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p],
+    ),
+    "hkv_segmented_attention_bind2": (
+        _c_i32,
+        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+         _c_i32, ctypes.c_float, _c_i32, _c_i32, _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64,
+         _c_p],
     ),
     "hkv_segmented_attention_call": (_c_i32, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "hkv_segmented_attention_plan": (

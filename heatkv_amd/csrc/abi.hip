@@ -81,6 +81,7 @@ extern "C" {
 
 // 0.2.0: hkv_segmented_attention's dot modes and work plan arguments, the
 // split-row K dtype; a work plan with no units is refused.
+// 0.3.0: hkv_segmented_attention_append2 / _bind2 (a second append destination).
 int32_t hkv_version(void) { return HKV_VERSION; }
 
 int32_t hkv_device_ok(int32_t device) {
@@ -192,7 +193,9 @@ int32_t build_attention_args(hkv::AttnArgs& a, bool check_tensors, const void* q
                                       int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
                                       int32_t qk_dot_mode, int32_t value_dot_mode,
                                       const int32_t* work_plan, int32_t plan_units,
-                                      void* workspace, int64_t workspace_bytes, const int32_t* append_offsets) {
+                                      void* workspace, int64_t workspace_bytes, const int32_t* append_offsets,
+                                      void* slab2_k = nullptr, void* slab2_v = nullptr, int64_t slab2_capacity = 0,
+                                      const int32_t* append2_offsets = nullptr) {
   (void)use_exp2;  // exp and exp2 modes are the same function; the kernel folds log2(e)
   if (qk_dot_mode < 0 || qk_dot_mode > 2)
     return fail(HKV_ERR_INVALID_ARG, "qk_dot_mode must be 0 (bf16), 1 (tf32) or 2 (fp32) (got %d)", qk_dot_mode);
@@ -265,6 +268,18 @@ int32_t build_attention_args(hkv::AttnArgs& a, bool check_tensors, const void* q
       return fail(HKV_ERR_INVALID_ARG,
                   "the append needs slab_capacity >= current_len and 16-byte aligned slab and current tensors");
   }
+  if (append2_offsets != nullptr) {
+    // the second destination of the append: always bound with its tensors
+    if (append_offsets == nullptr)
+      return fail(HKV_ERR_INVALID_ARG, "append2_offsets needs append_offsets (it repeats that append)");
+    if (!slab2_k || !slab2_v || slab2_capacity < cur_len ||
+        ((reinterpret_cast<uintptr_t>(slab2_k) | reinterpret_cast<uintptr_t>(slab2_v)) & 15) != 0)
+      return fail(HKV_ERR_INVALID_ARG,
+                  "the second append needs 16-byte aligned slab2 tensors and slab2_capacity >= current_len");
+    if (slab2_capacity * row_bytes >= 0x7fffffffLL)
+      return fail(HKV_ERR_UNSUPPORTED, "slab2 rows per batch row must stay below %lld",
+                  static_cast<long long>(0x7fffffffLL / row_bytes));
+  }
   a = hkv::AttnArgs{};
   a.q = q;
   a.slab_k = slab_k;
@@ -293,6 +308,10 @@ int32_t build_attention_args(hkv::AttnArgs& a, bool check_tensors, const void* q
   a.plan = work_plan;
   a.plan_units = work_plan != nullptr ? plan_units : 0;
   a.append_offsets = append_offsets;
+  a.append2_offsets = append2_offsets;
+  a.slab2_k = append2_offsets != nullptr ? slab2_k : nullptr;
+  a.slab2_v = append2_offsets != nullptr ? slab2_v : nullptr;
+  a.slab2_capacity = append2_offsets != nullptr ? slab2_capacity : 0;
   return 0;
 }
 }  // namespace
@@ -313,6 +332,31 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
       a, true, q, slab_k, slab_v, seg_starts, seg_ends, seg_counts, cur_k, cur_v, out, lse, batch, heads, cur_len,
       slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype, softmax_scale, use_exp2,
       qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes, append_offsets);
+  if (code != 0) return code;
+  const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(HKV_ERR_LAUNCH, "segmented attention launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int32_t hkv_segmented_attention_append2(const void* q, void* slab_k, void* slab_v,
+                                       const int32_t* seg_starts, const int32_t* seg_ends,
+                                       const int32_t* seg_counts, const void* cur_k, const void* cur_v,
+                                       void* out, float* lse, int32_t batch, int32_t heads,
+                                       int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                       int32_t head_dim, int32_t q_dtype, int32_t k_dtype,
+                                       int32_t v_dtype, int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                       int32_t qk_dot_mode, int32_t value_dot_mode,
+                                       const int32_t* work_plan, int32_t plan_units,
+                                       void* workspace, int64_t workspace_bytes, const int32_t* append_offsets,
+                                       void* slab2_k, void* slab2_v, int64_t slab2_capacity,
+                                       const int32_t* append2_offsets, void* stream) {
+  hkv::AttnArgs a{};
+  const int32_t code = build_attention_args(
+      a, true, q, slab_k, slab_v, seg_starts, seg_ends, seg_counts, cur_k, cur_v, out, lse, batch, heads, cur_len,
+      slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype, softmax_scale, use_exp2,
+      qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes, append_offsets, slab2_k,
+      slab2_v, slab2_capacity, append2_offsets);
   if (code != 0) return code;
   const hipError_t e = hkv::launch_segmented_attention(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
@@ -353,6 +397,34 @@ int32_t hkv_segmented_attention_bind(void* bound, int64_t bound_bytes, const int
       batch, heads, cur_len, slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype,
       softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes,
       append_offsets);
+  if (code != 0) return code;
+  b->device = device;
+  b->tag = kBoundTag;
+  return ok();
+}
+
+int32_t hkv_segmented_attention_bind2(void* bound, int64_t bound_bytes, const int32_t* seg_starts,
+                                      const int32_t* seg_ends, const int32_t* seg_counts, int32_t batch,
+                                      int32_t heads, int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                      int32_t head_dim, int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                      int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                      int32_t qk_dot_mode, int32_t value_dot_mode, const int32_t* work_plan,
+                                      int32_t plan_units, void* workspace, int64_t workspace_bytes,
+                                      const int32_t* append_offsets, void* slab2_k, void* slab2_v,
+                                      int64_t slab2_capacity, const int32_t* append2_offsets) {
+  if (bound == nullptr || bound_bytes < static_cast<int64_t>(sizeof(BoundAttention)) ||
+      (reinterpret_cast<uintptr_t>(bound) & 7) != 0)
+    return fail(HKV_ERR_INVALID_ARG, "bound must point to %d bytes, 8-byte aligned (hkv_segmented_attention_bound_bytes)",
+                static_cast<int>(sizeof(BoundAttention)));
+  BoundAttention* b = static_cast<BoundAttention*>(bound);
+  b->tag = 0;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(HKV_ERR_DEVICE, "hipGetDevice failed");
+  const int32_t code = build_attention_args(
+      b->a, false, nullptr, nullptr, nullptr, seg_starts, seg_ends, seg_counts, nullptr, nullptr, nullptr, nullptr,
+      batch, heads, cur_len, slab_capacity, max_segments, head_dim, q_dtype, k_dtype, v_dtype, out_dtype,
+      softmax_scale, use_exp2, qk_dot_mode, value_dot_mode, work_plan, plan_units, workspace, workspace_bytes,
+      append_offsets, slab2_k, slab2_v, slab2_capacity, append2_offsets);
   if (code != 0) return code;
   b->device = device;
   b->tag = kBoundTag;

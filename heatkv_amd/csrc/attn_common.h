@@ -859,12 +859,14 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The current rows' append (AttnArgs::append_offsets).  A copy block moves
-// kAppendRows rows of K and of V of one (b, h), 16 bytes per lane per access
-// (one access per lane and tensor for 16-bit rows); heads with off < 0 or
-// off + L > capacity are skipped.  The rows written lie outside every segment
-// the launch reads (the caller's contract), so copy blocks and attention
-// workgroups of one launch need no ordering.
+// The current rows' append (AttnArgs::append_offsets, and the second
+// destination append2_offsets).  A copy block moves kAppendRows rows of K and
+// of V of one (b, h), 16 bytes per lane per access (one access per lane and
+// tensor for 16-bit rows), read once and written to each destination; a
+// destination with off < 0 or off + L > its capacity is skipped.  The rows
+// written lie outside every segment the launch reads (the caller's
+// contract), so copy blocks and attention workgroups of one launch need no
+// ordering.
 constexpr int kAppendRows = 16;
 
 __host__ __device__ inline int64_t append_blocks(int32_t batch, int32_t heads, int32_t L) {
@@ -883,15 +885,22 @@ __device__ __forceinline__ void append_block(const AttnArgs& a, uint32_t blk, in
   const int32_t h = static_cast<int32_t>(bh % H);
   const int64_t b = bh / H;
   const int32_t off = a.append_offsets[h];
-  if (off < 0 || off > cap - L) return;
+  const bool w1 = off >= 0 && off <= cap - L;
+  const int64_t cap2 = a.slab2_capacity;
+  const int32_t off2 = a.append2_offsets != nullptr ? a.append2_offsets[h] : -1;
+  const bool w2 = off2 >= 0 && off2 <= cap2 - L;
+  if (!w1 && !w2) return;
   const int32_t r0 = static_cast<int32_t>(blk - bh * chunks) * kAppendRows;
   const int32_t rows = L - r0 < kAppendRows ? L - r0 : kAppendRows;
   const int64_t dst_row = b * cap + off + r0;
+  const int64_t dst2_row = b * cap2 + off2 + r0;
   const int64_t src_row = static_cast<int64_t>(bh) * L + r0;
   const uint4* sk = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.cur_k) + src_row * k_row);
   const uint4* sv = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.cur_v) + src_row * v_row);
   uint4* dk = reinterpret_cast<uint4*>(static_cast<uint8_t*>(const_cast<void*>(a.slab_k)) + dst_row * k_row);
   uint4* dv = reinterpret_cast<uint4*>(static_cast<uint8_t*>(const_cast<void*>(a.slab_v)) + dst_row * v_row);
+  uint4* dk2 = reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.slab2_k) + dst2_row * k_row);
+  uint4* dv2 = reinterpret_cast<uint4*>(static_cast<uint8_t*>(a.slab2_v) + dst2_row * v_row);
   const int32_t nk = rows * (k_row / 16);
   const int32_t nv = rows * (v_row / 16);
   // one access of each tensor in flight per lane: more (a deeper batch of
@@ -901,8 +910,10 @@ __device__ __forceinline__ void append_block(const AttnArgs& a, uint32_t blk, in
     uint4 xk, xv;
     if (u < nk) xk = sk[u];
     if (u < nv) xv = sv[u];
-    if (u < nk) dk[u] = xk;
-    if (u < nv) dv[u] = xv;
+    if (w1 && u < nk) dk[u] = xk;
+    if (w1 && u < nv) dv[u] = xv;
+    if (w2 && u < nk) dk2[u] = xk;
+    if (w2 && u < nv) dv2[u] = xv;
   }
 }
 

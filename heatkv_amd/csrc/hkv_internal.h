@@ -89,6 +89,13 @@ struct AttnArgs {
   // append_offsets[h] (-1: head h is not copied).
   const int32_t* append_offsets;
   int32_t append_first;     // first copy workgroup of a fused launch (set by the launch)
+  // A second destination of the same rows, or null: slab2 rows
+  // [off2, off2 + L) of batch row b, off2 = append2_offsets[h] (-1: none);
+  // slab2 has the dtypes of the slab.
+  const int32_t* append2_offsets;
+  void* slab2_k;
+  void* slab2_v;
+  int64_t slab2_capacity;
 };
 
 // Work plan units (build_attention_plan): head, index in the head

@@ -33,7 +33,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -393,6 +393,7 @@ def fused_real_pruning_flat_segmented_attention(
     work_plan: Optional[torch.Tensor] = None,
     append_offsets: Optional[torch.Tensor] = None,
     k_split_rows: bool = False,
+    append_also: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
     _bind: Optional[list] = None,
 ):
     """Attention of the current scale over the flat slab segments plus itself.
@@ -413,7 +414,12 @@ def fused_real_pruning_flat_segmented_attention(
     ``k_split_rows`` (an extension): q is fp32 and ``current_k`` /
     ``persisted_k`` are float32-typed tensors whose rows hold split rows of
     fp32 K (:func:`qkv_produce` with ``k_split_rows=True``), so the call skips
-    its own split of K; same results as passing the fp32 K.  ``_bind``
+    its own split of K; same results as passing the fp32 K.  ``append_also``
+    (an extension, with ``append_offsets``): ``(slab2_k, slab2_v, offsets2)``,
+    a second destination of the same rows -- ``[B, capacity2, D]`` tensors of
+    the slab's dtypes and int32 ``offsets2 [H]`` (-1: not written) -- written
+    by the same copy (a dense-prefix step that also fills the slab of the
+    first pruned target).  ``_bind``
     (internal): a list that receives what :class:`BoundSegmentedAttention`
     needs to repeat this launch.
     Mirrors fused_real_pruning_flat_segmented_attention
@@ -540,6 +546,23 @@ def fused_real_pruning_flat_segmented_attention(
         if persisted_k.dtype != current_k.dtype or persisted_v.dtype != current_v.dtype:
             raise ValueError("append_offsets: the slab and the current rows must share their dtypes")
         append_offsets = append_offsets.contiguous()
+    if append_also is not None:
+        if append_offsets is None:
+            raise ValueError("append_also repeats the append of append_offsets; pass both")
+        slab2_k, slab2_v, offsets2 = append_also
+        if (slab2_k.ndim != 3 or slab2_k.shape != slab2_v.shape or slab2_k.shape[0] != batch_size
+                or slab2_k.shape[2] != head_dim):
+            raise ValueError("append_also: slab2_k and slab2_v must be [B, capacity2, D] tensors of one shape")
+        if slab2_k.dtype != current_k.dtype or slab2_v.dtype != current_v.dtype:
+            raise ValueError("append_also: the second slab and the current rows must share their dtypes")
+        if slab2_k.device != q.device or slab2_v.device != q.device:
+            raise ValueError("append_also: the second slab must be on q's device")
+        if not (slab2_k.is_contiguous() and slab2_v.is_contiguous()):
+            raise ValueError("append_also: the second slab must be contiguous (the append writes it in place)")
+        if (offsets2.dtype != torch.int32 or tuple(offsets2.shape) != (num_heads,)
+                or offsets2.device != q.device):
+            raise ValueError("append_also: its offsets must be an int32 tensor [H] on q's device")
+        offsets2 = offsets2.contiguous()
     stream = torch.cuda.current_stream(q.device)
     ws = _lib.attention_workspace(q.device, stream)
     k_code = _lib.dtype_code(current_k.dtype)
@@ -566,9 +589,13 @@ def fused_real_pruning_flat_segmented_attention(
     lib = _lib.load()
     if append_offsets is None:
         fn = lib.hkv_segmented_attention
-    else:
+    elif append_also is None:
         fn = lib.hkv_segmented_attention_append
         args.append(append_offsets.data_ptr())
+    else:
+        fn = lib.hkv_segmented_attention_append2
+        args += [append_offsets.data_ptr(), slab2_k.data_ptr(), slab2_v.data_ptr(), int(slab2_k.shape[1]),
+                 offsets2.data_ptr()]
     args.append(stream.cuda_stream)
     _lib.check(fn(*args))
     if _bind is not None:
@@ -576,7 +603,7 @@ def fused_real_pruning_flat_segmented_attention(
         # / slab tensors of the same shapes (None when this call converted its
         # inputs: those copies are per call)
         keep = (q, persisted_k, persisted_v, current_k, current_v, segment_starts, segment_ends, segment_counts,
-                work_plan, append_offsets, ws)
+                work_plan, append_offsets, ws, append_also)
         _bind.append(None if converted or lse is not None else (fn, args, output.shape, out_dtype, keep))
     if return_lse:
         return output, lse
@@ -607,9 +634,15 @@ class BoundSegmentedAttention:
         self._block = (ctypes.c_int64 * ((size + 7) // 8))()
         self._addr = ctypes.addressof(self._block)
         append = a[28] if len(a) > 29 else None
-        _lib.check(lib.hkv_segmented_attention_bind(
-            self._addr, size, a[3], a[4], a[5], a[10], a[11], a[12], a[13], a[14], a[15], a[16], a[17], a[18],
-            a[19], a[20], a[21], a[22], a[23], a[24], a[25], a[26], a[27], append))
+        if len(a) > 30:
+            # the second append destination (slab2 K/V, capacity, offsets) is bound with the rest
+            _lib.check(lib.hkv_segmented_attention_bind2(
+                self._addr, size, a[3], a[4], a[5], a[10], a[11], a[12], a[13], a[14], a[15], a[16], a[17], a[18],
+                a[19], a[20], a[21], a[22], a[23], a[24], a[25], a[26], a[27], append, a[29], a[30], a[31], a[32]))
+        else:
+            _lib.check(lib.hkv_segmented_attention_bind(
+                self._addr, size, a[3], a[4], a[5], a[10], a[11], a[12], a[13], a[14], a[15], a[16], a[17], a[18],
+                a[19], a[20], a[21], a[22], a[23], a[24], a[25], a[26], a[27], append))
         self._call = lib.hkv_segmented_attention_call
         self._out_shape = tuple(out_shape)
         self._out_dtype = out_dtype

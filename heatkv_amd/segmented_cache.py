@@ -131,9 +131,10 @@ class _StepReplay:
     be repeated as bound; the caller then takes the full step."""
 
     __slots__ = ("args", "kind", "attn", "old_len", "new_len", "final", "k_split_rows", "copy", "activate",
-                 "buf_shapes")
+                 "buf_shapes", "dual", "scale")
 
-    def __init__(self, args, kind, attn, old_len, new_len, final, copy=None, activate=None, buf_shapes=None):
+    def __init__(self, args, kind, attn, old_len, new_len, final, copy=None, activate=None, buf_shapes=None,
+                 dual=False, scale=-1):
         self.args = args  # the step's (out_dtype, softmax_scale, softmax_mode, appended, k_split_rows)
         k_split_rows = bool(args[4])
         self.kind = kind  # "slab": segmented step; "dense": dense prefix kept in place
@@ -145,6 +146,8 @@ class _StepReplay:
         self.copy = copy  # (plan, tag) of the residual append, or None
         self.activate = activate  # target whose slab is packed after a dense step, or None
         self.buf_shapes = buf_shapes  # ((shape, dtype), (shape, dtype)) of the dense buffer
+        self.dual = dual  # the launch also wrote the rows into the slab (dense step; the bound slab storage)
+        self.scale = scale
 
     def run(self, cache: "SegmentedLayerCache", q, k, v):
         if cache.logical_len != self.old_len:
@@ -186,8 +189,9 @@ class _StepReplay:
             cache.reset()
             return out
         cache.logical_len = self.new_len
+        cache._dual_next = self.scale + 1 if self.dual and cache._dual_next == self.scale else -1
         if self.activate is not None:
-            cache._activate_from_dense(buf_k, buf_v, self.activate)
+            cache._activate_after_dense(buf_k, buf_v, self.activate)
             cache.dense_buf = None
             cache._dense_views = None
         return out
@@ -208,6 +212,9 @@ class SegmentedLayerCache:
         self._replays: Dict[int, _StepReplay] = {}
         self._packs: Dict[tuple, BoundPack] = {}  # bound slab copies, by copy tag
         self._knobs: Optional[tuple] = None
+        # the slab's storage, kept for the next generations (same shape and
+        # dtypes): bound second appends of dense steps refer to it
+        self._slab_store: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self.reset()
 
     # ------------------------------------------------------------------ state
@@ -225,14 +232,30 @@ class SegmentedLayerCache:
         # dense scale, each step's rows written by its attention launch
         self.dense_buf: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self._dense_views = None  # dense_buf seen as slabs [B, H*rows, D] (replayed steps)
+        # the next dense scale whose rows the in-place steps also wrote into
+        # the slab storage (-1: a step did not), so the activation has nothing to pack
+        self._dual_next = 0
+
+    def _slab_storage(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The slab's K/V storage ``[B, capacity, D]``, allocated when its shape,
+        dtypes or device change and kept across generations (the reference
+        allocates it per generation, :1092-1144; contents of unowned rows are
+        undefined either way).  A new storage drops the recorded steps, whose
+        bound second appends point at the old one."""
+        cap = int(self.schedule.capacity)
+        st = self._slab_store
+        if (st is None or tuple(st[0].shape) != (batch, cap, head_dim) or st[0].dtype != k_dtype
+                or st[1].dtype != v_dtype or st[0].device != torch.device(device)):
+            st = self._slab_store = (torch.empty((batch, cap, head_dim), device=device, dtype=k_dtype),
+                                     torch.empty((batch, cap, head_dim), device=device, dtype=v_dtype))
+            self._replays.clear()
+            prof.stat_add("storage_allocations")
+            prof.stat_add("storage_capacity_slots", cap)
+        return st
 
     def _ensure_slab(self, batch: int, head_dim: int, device, k_dtype, v_dtype) -> None:
-        """Slab K/V ``[B, capacity, D]`` (:1092-1144); contents of unowned rows are undefined."""
-        cap = int(self.schedule.capacity)
-        self.cached_k = torch.empty((batch, cap, head_dim), device=device, dtype=k_dtype)
-        self.cached_v = torch.empty((batch, cap, head_dim), device=device, dtype=v_dtype)
-        prof.stat_add("storage_allocations")
-        prof.stat_add("storage_capacity_slots", cap)
+        """Slab K/V ``[B, capacity, D]`` (:1092-1144) as the cache."""
+        self.cached_k, self.cached_v = self._slab_storage(batch, head_dim, device, k_dtype, v_dtype)
 
     # ------------------------------------------------------------------ copies
 
@@ -261,6 +284,36 @@ class SegmentedLayerCache:
                 self._packs[tag] = bound
         else:
             pack_flat_segments_kv(**kw)
+
+    def _activate_after_dense(self, dense_k, dense_v, target: int) -> None:
+        """The slab becomes the cache at ``target``: when every dense step of
+        this generation also wrote its rows into the slab storage, there is
+        nothing left to pack; else the dense cache is packed."""
+        if self._dual_next == target and self._slab_store is not None:
+            B, H, T, D = dense_k.shape
+            self._ensure_slab(B, D, dense_k.device, dense_k.dtype, dense_v.dtype)
+            self.active = True
+            prof.stat_add("static_pack_state_calls")
+            return
+        self._activate_from_dense(dense_k, dense_v, target)
+
+    def _activation_target(self) -> Optional[int]:
+        """The first target with removed heads (the slab's activation), or None."""
+        return next((t for t in range(1, self.num_scales) if has_removed(self.removed(t))), None)
+
+    def _dual_offsets(self, target: int, scale: int, heads: int, device) -> torch.Tensor:
+        """Slab offsets of scale ``scale``'s rows of each head at ``target``
+        (-1: not live there), on ``device``, made once: where the in-place
+        dense step of ``scale`` also writes its rows."""
+        key = ("dual", int(target), int(scale), heads, str(device))
+        hit = self._tables_by_len.get(key)
+        if hit is None:
+            offs = torch.full((heads,), -1, dtype=torch.int32)
+            for seg in self.schedule.live_segments(int(target)):
+                if seg.source_scale == scale and 0 <= seg.head < heads:
+                    offs[seg.head] = int(seg.offset)
+            hit = self._tables_by_len[key] = offs.to(device)
+        return hit
 
     def _activate_from_dense(self, dense_k, dense_v, target: int) -> None:
         """Pack the dense cache into a new slab for ``target`` (:1639-1711)."""
@@ -373,6 +426,14 @@ class SegmentedLayerCache:
                   persisted_v=buf_v.reshape(B, H * cap, buf_v.shape[3]), segment_starts=st, segment_ends=en,
                   segment_counts=ct, current_k=k, current_v=v, softmax_scale=scale, softmax_mode=mode,
                   out_dtype=out_dtype, work_plan=plan, append_offsets=offs, k_split_rows=self.k_split_rows)
+        # the same launch also writes the step's rows into the slab storage at
+        # their offsets of the activation target, so that target packs nothing
+        act = self._activation_target()
+        dual = store and act is not None and scale_ind < act and self._dual_next == scale_ind
+        if dual:
+            slab_k, slab_v = self._slab_storage(B, k.shape[3], k.device, k.dtype, v.dtype)
+            kw["append_also"] = (slab_k, slab_v, self._dual_offsets(act, scale_ind, H, q.device))
+        self._dual_next = scale_ind + 1 if dual else -1
         bound = None
         with prof.phase("attention"):
             if record is not None:
@@ -389,13 +450,14 @@ class SegmentedLayerCache:
                     raise RuntimeError("dense prefix packed into the slab before its buffer is full")
                 activate = scale_ind + 1
                 with prof.phase("compact"):
-                    self._activate_from_dense(buf_k, buf_v, activate)
+                    self._activate_after_dense(buf_k, buf_v, activate)
                 self.dense_buf = None
                 self._dense_views = None
         if bound is not None:
             self._replays[scale_ind] = _StepReplay(
                 record, "dense", bound, old_len, old_len + L, final,
-                activate=activate, buf_shapes=((tuple(buf_k.shape), buf_k.dtype), (tuple(buf_v.shape), buf_v.dtype)))
+                activate=activate, buf_shapes=((tuple(buf_k.shape), buf_k.dtype), (tuple(buf_v.shape), buf_v.dtype)),
+                dual=dual, scale=scale_ind)
         return out
 
     # ------------------------------------------------------------------ attention

@@ -50,7 +50,7 @@ int32_t hkv_concat_kv(const void* old_k, const void* new_k, const void* old_v, c
 /* Library version, (major << 16) | (minor << 8) | patch: HKV_VERSION of the
  * header the library was built with.  A loader compares it with the version
  * of the header (or bindings) it was written against and refuses a mismatch. */
-#define HKV_VERSION ((0 << 16) | (2 << 8) | 0)
+#define HKV_VERSION ((0 << 16) | (3 << 8) | 0)
 int32_t hkv_version(void);
 
 /* 1 when `device` is a gfx950 GPU this build can run on, else 0.
@@ -193,6 +193,33 @@ int32_t hkv_segmented_attention_append(const void* q, void* slab_k, void* slab_v
                                        void* workspace, int64_t workspace_bytes,
                                        const int32_t* append_offsets, void* stream);
 
+/*
+ * hkv_segmented_attention_append whose copy also writes the same rows to a
+ * second slab: current rows [0, cur_len) of (b, h) go to rows
+ * [off, off + cur_len) of batch row b of slab2_k / slab2_v ([B,
+ * slab2_capacity, D], the dtypes of slab_k / slab_v), off =
+ * append2_offsets[h] (-1: not written), read once for both destinations.
+ * Needs append_offsets; slab2 16-byte aligned, slab2_capacity >= cur_len, and
+ * its written rows outside every row the launch reads.  No reference
+ * counterpart: a dense-prefix step (enable_real_pruning_fast.py:1972-2038)
+ * keeps its rows in the dense cache for the next dense step and puts them in
+ * the slab of the first pruned target at once, so that target's activation
+ * pack (:1639-1711) has nothing left to copy.
+ */
+int32_t hkv_segmented_attention_append2(const void* q, void* slab_k, void* slab_v,
+                                        const int32_t* seg_starts, const int32_t* seg_ends,
+                                        const int32_t* seg_counts, const void* cur_k,
+                                        const void* cur_v, void* out, float* lse,
+                                        int32_t batch, int32_t heads, int32_t cur_len,
+                                        int64_t slab_capacity, int32_t max_segments, int32_t head_dim,
+                                        int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                        int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                        int32_t qk_dot_mode, int32_t value_dot_mode,
+                                        const int32_t* work_plan, int32_t plan_units,
+                                        void* workspace, int64_t workspace_bytes,
+                                        const int32_t* append_offsets, void* slab2_k, void* slab2_v,
+                                        int64_t slab2_capacity, const int32_t* append2_offsets, void* stream);
+
 /* A bound attention call: hkv_segmented_attention_append's arguments other
  * than the tensors (tables, shapes, dtypes, scale, dot modes, work plan,
  * workspace and append offsets) validated once into a caller-owned block of
@@ -214,6 +241,18 @@ int32_t hkv_segmented_attention_bind(void* bound, int64_t bound_bytes, const int
                                      int32_t out_dtype, float softmax_scale, int32_t use_exp2, int32_t qk_dot_mode,
                                      int32_t value_dot_mode, const int32_t* work_plan, int32_t plan_units,
                                      void* workspace, int64_t workspace_bytes, const int32_t* append_offsets);
+/* hkv_segmented_attention_bind with hkv_segmented_attention_append2's second
+ * destination, bound with the rest: slab2_k / slab2_v stay the same tensors
+ * for every call of the block. */
+int32_t hkv_segmented_attention_bind2(void* bound, int64_t bound_bytes, const int32_t* seg_starts,
+                                      const int32_t* seg_ends, const int32_t* seg_counts, int32_t batch,
+                                      int32_t heads, int32_t cur_len, int64_t slab_capacity, int32_t max_segments,
+                                      int32_t head_dim, int32_t q_dtype, int32_t k_dtype, int32_t v_dtype,
+                                      int32_t out_dtype, float softmax_scale, int32_t use_exp2,
+                                      int32_t qk_dot_mode, int32_t value_dot_mode, const int32_t* work_plan,
+                                      int32_t plan_units, void* workspace, int64_t workspace_bytes,
+                                      const int32_t* append_offsets, void* slab2_k, void* slab2_v,
+                                      int64_t slab2_capacity, const int32_t* append2_offsets);
 int32_t hkv_segmented_attention_call(const void* bound, const void* q, void* slab_k, void* slab_v,
                                      const void* cur_k, const void* cur_v, void* out, void* stream);
 

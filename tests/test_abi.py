@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_host_only_calls():
     lib = _lib.load()
-    assert lib.hkv_version() == 0x000200 == _lib.ABI_VERSION
+    assert lib.hkv_version() == 0x000300 == _lib.ABI_VERSION
     assert lib.hkv_device_ok(-1) == 0
     assert isinstance(_lib.last_error(), str)
 

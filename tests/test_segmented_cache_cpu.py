@@ -24,15 +24,21 @@ from oracle import segmented_attention as oattn
 
 
 def _cpu_attention(*, q, persisted_k, persisted_v, segment_starts, segment_ends, segment_counts,
-                   current_k, current_v, softmax_scale, softmax_mode="exp", append_offsets=None, **_):
+                   current_k, current_v, softmax_scale, softmax_mode="exp", append_offsets=None, append_also=None,
+                   **_):
     if append_offsets is not None:
-        # the fused append, written before the attention reads the slab: a
-        # row that a segment of this call covered would change the result
+        # the fused append (and its second destination), written before the
+        # attention reads the slab: a row that a segment of this call covered
+        # would change the result
         L = current_k.shape[2]
-        for h, off in enumerate(append_offsets.tolist()):
-            if 0 <= off <= persisted_k.shape[1] - L:
-                persisted_k[:, off:off + L] = current_k[:, h]
-                persisted_v[:, off:off + L] = current_v[:, h]
+        dests = [(persisted_k, persisted_v, append_offsets)]
+        if append_also is not None:
+            dests.append(append_also)
+        for dk, dv, offs in dests:
+            for h, off in enumerate(offs.tolist()):
+                if 0 <= off <= dk.shape[1] - L:
+                    dk[:, off:off + L] = current_k[:, h]
+                    dv[:, off:off + L] = current_v[:, h]
     f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
     out, _ = oattn.flat_segmented_attention(
         f(q), f(persisted_k), f(persisted_v), segment_starts.numpy(), segment_ends.numpy(),
