@@ -657,6 +657,62 @@ def test_attention_fused_append(seed, qkdt, vdt, planned, split, device, monkeyp
     assert np.array_equal(bits(slab_v), bits(want_v))
 
 
+@pytest.mark.parametrize("seed,qkdt,vdt,planned", [
+    (95, torch.bfloat16, torch.bfloat16, True), (96, torch.float16, torch.float16, False),
+    (97, torch.float32, torch.float32, True)])
+def test_attention_fused_append_two_destinations(seed, qkdt, vdt, planned, device, monkeypatch):
+    """append_also (hkv_segmented_attention_append2): the output and LSE equal
+    the plain call's bit for bit, the first slab equals the one-destination
+    append's, and the second slab equals itself with each head's current rows
+    written at its own offset (heads at -1 and one past the second capacity
+    untouched); the 16-bit kernel copies in its own launch, the staged kernel
+    (fp32) after it."""
+    from heatkv_amd import segmented_attention_plan
+
+    monkeypatch.setenv("HKV_ATTN_SPLIT_ROWS", "0")
+    g = torch.Generator().manual_seed(seed)
+    B, H, L, cap0, S = 2, 6, 37, 500, 3
+    cap = cap0 + H * L
+    print(f"[attn] two-destination append seed={seed} {qkdt} {vdt} planned={planned}", flush=True)
+    q, sk0, sv0, tables, ck, cv = _random_case(seed, B, H, L, cap0, S, dtype=qkdt, kdtype=qkdt, vdtype=vdt)
+    sk = torch.cat((sk0, torch.randn((B, H * L, 128), generator=g).to(qkdt)), dim=1)
+    sv = torch.cat((sv0, torch.randn((B, H * L, 128), generator=g).to(vdt)), dim=1)
+    offsets = [cap0 + h * L for h in range(H)]
+    offsets[1] = -1
+    cap2 = 3 * H * L
+    s2k = torch.randn((B, cap2, 128), generator=g).to(qkdt)
+    s2v = torch.randn((B, cap2, 128), generator=g).to(vdt)
+    offsets2 = [int(x) for x in torch.randperm(3 * H, generator=g)[:H] * L]
+    offsets2[2] = -1
+    offsets2[3] = cap2 - L + 1  # past the second capacity: not written
+    want_k, want_v = sk.clone(), sv.clone()
+    want2_k, want2_v = s2k.clone(), s2v.clone()
+    for h in range(H):
+        if offsets[h] >= 0:
+            want_k[:, offsets[h]:offsets[h] + L] = ck[:, h]
+            want_v[:, offsets[h]:offsets[h] + L] = cv[:, h]
+        if 0 <= offsets2[h] <= cap2 - L:
+            want2_k[:, offsets2[h]:offsets2[h] + L] = ck[:, h]
+            want2_v[:, offsets2[h]:offsets2[h] + L] = cv[:, h]
+    plan = (segmented_attention_plan(*tables, batch_size=B, current_len=L, capacity=cap, device=device)
+            if planned else None)
+    scale = 1.0 / math.sqrt(128)
+    out_a, lse_a = _run(q, sk, sv, tables, ck, cv, scale, device, work_plan=plan)
+    slab_k, slab_v = sk.to(device), sv.to(device)
+    d2k, d2v = s2k.to(device), s2v.to(device)
+    out_b, lse_b = _run(q, slab_k, slab_v, tables, ck, cv, scale, device, work_plan=plan,
+                        append_offsets=torch.tensor(offsets, dtype=torch.int32, device=device),
+                        append_also=(d2k, d2v, torch.tensor(offsets2, dtype=torch.int32, device=device)))
+    assert np.array_equal(bits(out_b), bits(out_a))
+    assert np.array_equal(bits(lse_b), bits(lse_a))
+    assert np.array_equal(bits(slab_k), bits(want_k)) and np.array_equal(bits(slab_v), bits(want_v))
+    assert np.array_equal(bits(d2k), bits(want2_k)) and np.array_equal(bits(d2v), bits(want2_v))
+    # without append_offsets the second destination is refused
+    with pytest.raises(ValueError, match="append_offsets"):
+        _run(q, slab_k, slab_v, tables, ck, cv, scale, device,
+             append_also=(d2k, d2v, torch.tensor(offsets2, dtype=torch.int32, device=device)))
+
+
 def test_attention_fused_append_rejects(device, monkeypatch):
     """append_offsets is refused where the call would not write the caller's
     slab: the split-row K path (a split copy of the slab) and a slab that is
