@@ -494,10 +494,11 @@ struct Unit {
   int32_t parts;    // 1 or 2
   int32_t record;   // first record of the item (parts > 1)
   int32_t counter;  // counter of the item (parts > 1)
+  int32_t arrive;   // 1: the two parts count in first, the second writes no record (merge_parts)
 };
 
 __host__ __device__ __forceinline__ Unit split_unit(const RoundSplit& t, int32_t j) {
-  Unit u{j, 0, 1, 0, 0};
+  Unit u{j, 0, 1, 0, 0, 0};
   if (t.two == 0) return u;
   const int32_t lead = t.whole_first ? t.items - t.two : 0;  // whole items before the parts
   if (j < lead) {
@@ -763,8 +764,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // device's coherence point) and read by an agent-scope atomic load (sc1: read
 // from it).  The publishing workgroup waits for its stores to be acknowledged
 // (s_waitcnt vmcnt(0), which on gfx9 counts stores) and for every wave
-// (barrier) before its counter add is issued; the merging workgroup issues its
-// record loads only after it has seen the counter's returned value (barrier).
+// (barrier) before its counter add (for two parts: the ready mark) is issued;
+// the merging workgroup issues its record loads only after it has seen the
+// counter's value (the returned value, or for two parts the ready mark read
+// by its spin; then a barrier).
 // So the hardware orders the record before the counter.  The memory model's
 // way of saying it, an acq_rel counter add, adds a write-back and an
 // invalidate of the whole XCD L2 (buffer_wbl2 / buffer_inv sc1) per part,
@@ -777,12 +780,29 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Spins of the merging part's wait for the other part's record (each
+// s_sleep 1, ~64 cycles): the other part has counted itself in and is
+// resident, so its record lands within microseconds; the bound only keeps
+// the wait finite.
+constexpr int32_t kReadySpins = 1 << 22;
+
 // Part of a cut item: publish the partial record, count it in, and if it is
 // the item's last part to finish, merge every part and write the output.
 // A record holds 66 * kThreads floats (each thread's 64 accumulators, its
 // running max and its sum); item r's parts use records 2r and 2r + 1.  The
 // output goes through `stage` (32 * kOutPitch bytes per wave) when
 // kStageOut, else straight from registers.
+//
+// With un.arrive (plans of more units than resident slots, whose two parts
+// mostly run at different times) the two parts count themselves in first:
+// the first to arrive writes its record and then adds a second time
+// (ready); the second writes no record of its own -- it waits until the
+// counter shows both arrivals and the ready mark (3), then merges from its
+// registers and the other record (2B final step 298.9 vs 300.7 us, sweep
+// scale 11 117.0 vs 120.2 us).  Otherwise (parts that run side by side in
+// one round: there the waiting part would only wait for the other's record;
+// sweep scale 9 38.6 vs 34.6 us) every part publishes its record before
+// counting in, and the last to count merges.
 template <int QDT, int kThreads, bool kStageOut = true>
 __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc, const Unit& un,
                                             int32_t parts, const f32x16_t (&oacc)[4], float m_run,
@@ -792,7 +812,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   int32_t* const counters = static_cast<int32_t*>(a.workspace);
   float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
   float* const rec0 = records + static_cast<int64_t>(un.record) * (66 * kThreads);
-  {
+  auto publish = [&]() {
     float* const mine = rec0 + static_cast<int64_t>(un.part) * (66 * kThreads);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -800,14 +820,35 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
       for (int j = 0; j < 16; ++j) st_agent(mine + (db * 16 + j) * kThreads + tid, oacc[db][j]);
     st_agent(mine + 64 * kThreads + tid, m_run);
     st_agent(mine + 65 * kThreads + tid, l_run);
+    wait_vmcnt<0>();
+    __syncthreads();
+  };
+  if (parts == 2 && un.arrive != 0) {
+    if (tid == 0)
+      merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (merge_turn == 0) {
+      // first to arrive: publish, then the ready mark
+      publish();
+      if (tid == 0)
+        __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (tid == 0) {
+      for (int32_t i = 0; i < kReadySpins; ++i) {
+        if (__hip_atomic_load(counters + un.counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+  } else {
+    publish();
+    if (tid == 0)
+      merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+    __syncthreads();
+    if (!merge_turn) return;
   }
-  wait_vmcnt<0>();
-  __syncthreads();
-  if (tid == 0)
-    merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
-  __syncthreads();
-  if (!merge_turn) return;
   // Every part is published: combine the parts in part order (this part's
   // own values from registers, equal to its record), the same arithmetic
   // whichever part merges.

@@ -99,9 +99,11 @@ struct AttnArgs {
 };
 
 // Work plan units (build_attention_plan): head, index in the head
-// (b * n_qt + qt), key tiles [t0, t1), cut item (-1 = whole), part, and 1
+// (b * n_qt + qt), key tiles [t0, t1), cut item (-1 = whole), part, 1
 // when the launch's items differ in length (the 16-bit kernel then
-// alternates its wave priority by tile), else 0.
+// alternates its wave priority by tile) else 0, and 1 when the plan has more
+// units than resident slots (a cut item's parts count in before publishing:
+// attn::merge_parts) else 0.
 constexpr int kPlanInts = 8;
 int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
                              int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t bm, int32_t slots,

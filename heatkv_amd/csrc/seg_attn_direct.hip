@@ -167,6 +167,7 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
     un.parts = parts;
     un.record = cut ? 2 * pcut : 0;
     un.counter = cut ? pcut : 0;
+    un.arrive = cut && pu[7] != 0 ? 1 : 0;
   } else {
     un = split_unit(split, static_cast<int32_t>(blockIdx.x));
     if (split.two == 0) un.item = xcd_item(un.item, a.batch * H, n_qt);

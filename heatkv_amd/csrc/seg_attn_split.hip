@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const int3
   // part of a cut item, merged through the workspace), else the workgroup's
   // item in longest-first order.
   WorkItem w;
-  Unit un{0, 0, 1, 0, 0};
+  Unit un{0, 0, 1, 0, 0, 0};
   int32_t p0 = 0, p1 = 0;
   if (planned) {
     const int32_t ph = pu[0], pj = pu[1], pcut = pu[4], ppart = pu[5];
@@ -191,6 +191,7 @@ __global__ __launch_bounds__(kSThreads, 1) void seg_attn_split_kernel(const int3
     un.parts = cut ? 2 : 1;
     un.record = cut ? 2 * pcut : 0;
     un.counter = cut ? pcut : 0;
+    un.arrive = cut && pu[7] != 0 ? 1 : 0;
     load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
                                  seg_pref);
   } else {

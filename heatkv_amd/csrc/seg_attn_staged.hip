@@ -169,7 +169,7 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
   // key-range part of a cut item, merged through the workspace as in the
   // 16-bit kernel), else the workgroup's item in longest-first order.
   WorkItem w;
-  Unit un{0, 0, 1, 0, 0};
+  Unit un{0, 0, 1, 0, 0, 0};
   int32_t p0 = 0, p1 = 0;
   if (a.plan != nullptr) {
     const int32_t* pu = a.plan + static_cast<int64_t>(blockIdx.x) * kPlanInts;
@@ -186,6 +186,7 @@ __global__ __launch_bounds__(NW * 64, MINB) void seg_attn_staged_kernel(const At
     un.parts = cut ? 2 : 1;
     un.record = cut ? 2 * pcut : 0;
     un.counter = cut ? pcut : 0;
+    un.arrive = cut && pu[7] != 0 ? 1 : 0;
     load_head_segments<kThreads>(a.seg_starts, a.seg_ends, a.seg_counts, cap, a.max_segments, w, seg_start,
                                  seg_pref);
   } else {

@@ -274,7 +274,10 @@ int32_t hkv_segmented_attention_call(const void* bound, const void* q, void* sla
  * first and end key tile, cut index (-1 = whole item), part (0 or 1), a flag
  * (1 when the items' key tile counts differ by more than 5/4: the 16-bit
  * kernel then alternates its wave priority by tile so the two workgroups of a
- * CU share its SIMDs evenly; 0 otherwise and in empty units), 0.
+ * CU share its SIMDs evenly; 0 otherwise and in empty units), and a flag (1
+ * when the plan has more units than slots: a cut item's two parts then count
+ * in before the first publishes its partial result and the second merges
+ * without publishing its own; 0 otherwise and in empty units).
  * Host-only: no device call.  No counterpart in the reference (its tables
  * are the whole plan: the Triton grid walks them).
  */
