@@ -54,8 +54,19 @@ def per_dispatch(path: str, kernel_substr: str) -> Dict[str, List[float]]:
     return dict(out)
 
 
-def stats_markdown(kt_dir: str, cmd: str) -> str:
-    paths = glob.glob(os.path.join(kt_dir, "*kernel_stats.csv"))
+def window_durations(kt_dir: str, kernel_substr: str) -> List[float]:
+    """Durations (us) of every dispatch of ``kernel_substr`` in dispatch order
+    (the ``*kernel_trace.csv`` of a ``--kernel-trace`` run)."""
+    paths = glob.glob(os.path.join(kt_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise FileNotFoundError(f"no *kernel_trace.csv under {kt_dir}")
+    rows = [r for r in _rows(paths[0]) if kernel_substr in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows]
+
+
+def stats_markdown(kt_dir: str, cmd: str, window_kernel: str = "", window: int = 0) -> str:
+    paths = glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True)
     if not paths:
         raise FileNotFoundError(f"no *kernel_stats.csv under {kt_dir}")
     lines = [
@@ -63,6 +74,20 @@ def stats_markdown(kt_dir: str, cmd: str) -> str:
         "",
         f"Command: `{cmd}`",
         "",
+    ]
+    if window_kernel and window > 0:
+        d = window_durations(kt_dir, window_kernel)
+        lines += [
+            f"`{window_kernel}` dispatches (all of the run, and its last {window}):",
+            "",
+            "| dispatches | mean us | median us | min us | max us |",
+            "|---|---:|---:|---:|---:|",
+        ]
+        for label, xs in ((f"all {len(d)}", d), (f"last {window}", d[-window:])):
+            lines.append(f"| {label} | {statistics.mean(xs):.2f} | {statistics.median(xs):.2f} | "
+                         f"{min(xs):.2f} | {max(xs):.2f} |")
+        lines.append("")
+    lines += [
         "| kernel | calls | avg us | min us | max us | share % |",
         "|---|---:|---:|---:|---:|---:|",
     ]
@@ -120,7 +145,7 @@ def group_summary(trace_dir: str, fetch_csv: str, write_csv: str, kernel_substr:
             "write_factor": t["write_factor"]}
 
 
-def counters_markdown(paths: List[str], kernel_substr: str, cmd: str) -> str:
+def counters_markdown(paths: List[str], kernel_substr: str, cmd: str, mean_us: float = 0.0) -> str:
     vals: Dict[str, List[float]] = {}
     for p in paths:
         vals.update(per_dispatch(p, kernel_substr))
@@ -134,6 +159,32 @@ def counters_markdown(paths: List[str], kernel_substr: str, cmd: str) -> str:
     ]
     for k in sorted(vals):
         lines.append(f"| {k} | {statistics.mean(vals[k]):.0f} | {len(vals[k])} |")
+    m = {k: statistics.mean(v) for k, v in vals.items()}
+    derived = []
+    if "GRBM_GUI_ACTIVE" in m:
+        # GRBM_GUI_ACTIVE counts the 8 XCDs; SQ cycle counters sum the 1024 SIMDs
+        cycles = m["GRBM_GUI_ACTIVE"] / 8.0
+        derived.append(f"cycles per dispatch {cycles:.0f}")
+        if mean_us:
+            derived.append(f"clock under load {cycles / (mean_us * 1e3):.2f} GHz over a {mean_us:.2f} us mean dispatch")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m:
+            derived.append(f"MFMA busy per SIMD {m['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024.0 / cycles:.3f}")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in m and "SQ_VALU_MFMA_COEXEC_CYCLES" in m:
+        derived.append("VALU co-executing with MFMA: "
+                       f"{m['SQ_VALU_MFMA_COEXEC_CYCLES'] / m['SQ_VALU_MFMA_BUSY_CYCLES']:.3f} of MFMA busy cycles")
+    if "SQ_INSTS_MFMA" in m and m["SQ_INSTS_MFMA"] > 0:
+        n = m["SQ_INSTS_MFMA"]
+        if "SQ_INSTS_VALU" in m:
+            trans = m.get("SQ_INSTS_VALU_TRANS_F32", 0.0)
+            derived.append(f"non-MFMA VALU instructions per MFMA {(m['SQ_INSTS_VALU'] - n) / n:.2f} "
+                           f"(of them transcendental {trans / n:.2f})")
+        for key, label in (("SQ_INSTS_LDS", "LDS"), ("SQ_INSTS_SALU", "SALU")):
+            if key in m:
+                derived.append(f"{label} instructions per MFMA {m[key] / n:.2f}")
+    if "SQ_WAIT_ANY" in m and "SQ_WAVE_CYCLES" in m:
+        derived.append(f"SQ_WAIT_ANY / SQ_WAVE_CYCLES {m['SQ_WAIT_ANY'] / m['SQ_WAVE_CYCLES']:.3f}")
+    if derived:
+        lines += ["", "Derived:", ""] + [f"* {x}" for x in derived]
     return "\n".join(lines) + "\n"
 
 
@@ -144,6 +195,8 @@ def main(argv=None):
     a.add_argument("kt_dir")
     a.add_argument("--out", required=True)
     a.add_argument("--cmd", required=True)
+    a.add_argument("--window-kernel", default="", help="also the last --window dispatches of this kernel")
+    a.add_argument("--window", type=int, default=0)
     b = sub.add_parser("traffic")
     b.add_argument("--fetch", required=True)
     b.add_argument("--write", required=True)
@@ -156,6 +209,7 @@ def main(argv=None):
     c.add_argument("--kernel", required=True)
     c.add_argument("--out", required=True)
     c.add_argument("--cmd", required=True)
+    c.add_argument("--mean-us", type=float, default=0.0, help="the kernel's mean dispatch time (for the clock)")
     d = sub.add_parser("group")
     d.add_argument("--trace", required=True)
     d.add_argument("--fetch", required=True)
@@ -168,14 +222,14 @@ def main(argv=None):
     d.add_argument("--cmd", required=True)
     args = ap.parse_args(argv)
     if args.what == "stats":
-        text = stats_markdown(args.kt_dir, args.cmd)
+        text = stats_markdown(args.kt_dir, args.cmd, args.window_kernel, args.window)
     elif args.what == "group":
         text = json.dumps(group_summary(args.trace, args.fetch, args.write, args.kernel, args.group,
                                         args.algo_bytes, args.calib_mib, args.cmd), indent=1) + "\n"
     elif args.what == "traffic":
         text = json.dumps(traffic(args.fetch, args.write, args.kernel, args.calib_mib, args.cmd), indent=1) + "\n"
     else:
-        text = counters_markdown(args.csv, args.kernel, args.cmd)
+        text = counters_markdown(args.csv, args.kernel, args.cmd, args.mean_us)
     os.makedirs(os.path.dirname(os.path.abspath(args.out)), exist_ok=True)
     with open(args.out, "w") as fh:
         fh.write(text)
