@@ -135,9 +135,10 @@ def test_unpruned_policy_stays_dense(cpu_ops):
 @pytest.mark.parametrize("fused_append", ["1", "0"])
 def test_dense_prefix_in_place_or_concatenated(cpu_ops, monkeypatch, fused_append):
     """With the fused append on, the dense prefix lives in one buffer sized
-    for every dense scale (each step's rows written by its attention call);
-    with it off, the cache concatenates as the reference does.  Same outputs
-    and the same packed slab either way."""
+    for every dense scale (each step's rows written by its attention call,
+    which also writes them into the slab, so the activation packs nothing);
+    with it off, the cache concatenates and packs as the reference does.
+    Same outputs and the same slab rows either way."""
     monkeypatch.setenv("HKV_FUSED_APPEND", fused_append)
     sides = (1, 2, 4, 6, 8)
     H, B, D = 3, 2, 16
@@ -149,6 +150,8 @@ def test_dense_prefix_in_place_or_concatenated(cpu_ops, monkeypatch, fused_appen
     sched = W.schedule_from_keep(keep, sides)
     cache = sc.SegmentedLayerCache(sched, W.removed_from_keep(keep, len(sides)), num_heads=H)
     inputs = W.generation_inputs(batch=B, heads=H, sides=sides, seed=9, dtype=torch.float32, head_dim=D)
+    packs = []
+    monkeypatch.setattr(sc, "pack_flat_segments_kv", lambda **kw: packs.append(kw["lengths"].tolist()) or _cpu_pack(**kw))
     for t, (q, k, v) in enumerate(inputs):
         out = cache.step(q, k, v, t, D ** -0.5)
         np.testing.assert_allclose(out.numpy(), _expected(inputs, keep, t, D ** -0.5), rtol=2e-5, atol=2e-5)
@@ -158,6 +161,13 @@ def test_dense_prefix_in_place_or_concatenated(cpu_ops, monkeypatch, fused_appen
                 assert cache.dense_buf[0].shape[2] == sum(s * s for s in sides[:4])
         elif t == 3:
             assert cache.active and cache.dense_buf is None
+            # in place, the dense steps' launches also wrote their rows into the
+            # slab (append_also), so the activation packed nothing; concatenated,
+            # the activation packs the dense cache
+            assert (len(packs) == 0) == (fused_append == "1")
+            for seg in sched.live_segments(4):
+                src = inputs[seg.source_scale][1][:, seg.head]
+                assert torch.equal(cache.cached_k[:, seg.offset:seg.offset + seg.length], src), seg
 
 
 @pytest.mark.parametrize("layer", [7, 0])
