@@ -151,7 +151,12 @@ def test_dense_prefix_in_place_or_concatenated(cpu_ops, monkeypatch, fused_appen
     cache = sc.SegmentedLayerCache(sched, W.removed_from_keep(keep, len(sides)), num_heads=H)
     inputs = W.generation_inputs(batch=B, heads=H, sides=sides, seed=9, dtype=torch.float32, head_dim=D)
     packs = []
-    monkeypatch.setattr(sc, "pack_flat_segments_kv", lambda **kw: packs.append(kw["lengths"].tolist()) or _cpu_pack(**kw))
+
+    def counting_pack(**kw):
+        packs.append(kw["lengths"].tolist())
+        return _cpu_pack(**kw)
+
+    monkeypatch.setattr(sc, "pack_flat_segments_kv", counting_pack)
     for t, (q, k, v) in enumerate(inputs):
         out = cache.step(q, k, v, t, D ** -0.5)
         np.testing.assert_allclose(out.numpy(), _expected(inputs, keep, t, D ** -0.5), rtol=2e-5, atol=2e-5)
