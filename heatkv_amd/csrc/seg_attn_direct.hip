@@ -335,15 +335,17 @@ __global__ __launch_bounds__(256, 2) void seg_attn_pipe_kernel(
   float m_run = -1e30f;
   float l_run = 0.f;
 
-  // S(t) = K(t) Q^T from stage t % 2
+  // S(t) = K(t) Q^T from stage t % 2, one key block's 8 k-steps after the
+  // other (each accumulator a chain of 8 MFMAs; 0.7-0.8 % faster on the 2B
+  // and 8B final steps than alternating the two blocks, same sums)
   auto qk = [&](f32x16_t (&sx)[2], int t) {
     const uint8_t* kst = ring + (t % NS) * kStageBytes + lane * 16;
     sx[0] = f32x16_t{};
     sx[1] = f32x16_t{};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int ks = 0; ks < 8; ++ks) {
         const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kst + (kb * 8 + ks) * 1024);
         sx[kb] = mfma32<MQK>(kf, qf[ks], sx[kb]);
       }
