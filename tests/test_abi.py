@@ -51,6 +51,16 @@ def test_version_and_host_only_calls():
     assert isinstance(_lib.last_error(), str)
 
 
+def test_header_and_integration_stub_carry_the_bindings_version():
+    """HKV_VERSION in the header and the version the integration guide's
+    ctypes stub checks are the one the bindings expect."""
+    m = re.search(r"#define\s+HKV_VERSION\s+\(\((\d+) << 16\) \| \((\d+) << 8\) \| (\d+)\)", open(HEADER).read())
+    assert m and (int(m.group(1)) << 16 | int(m.group(2)) << 8 | int(m.group(3))) == _lib.ABI_VERSION
+    guide = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    checks = re.findall(r"hkv_version\(\)\s*==\s*(0x[0-9a-fA-F]+)", guide)
+    assert checks and all(int(c, 16) == _lib.ABI_VERSION for c in checks)
+
+
 def test_argument_errors_before_any_device_call():
     lib = _lib.load()
     null = None
