@@ -36,9 +36,10 @@ FLAGS = [
 # Per-source flags.  The 16-bit and split-row attention kernels take their
 # work plan's pointer and unit count as their first two arguments, preloaded
 # into SGPRs at wave launch, so the unit's load needs no kernel-argument load
-# first.
+# first.  The 16-bit kernel keeps the pre-register-allocation schedule (no
+# post-RA machine scheduler): 0.3-1 % faster on every measured launch shape.
 EXTRA = {
-    "seg_attn_direct.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
+    "seg_attn_direct.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2", "-mllvm", "-enable-post-misched=0"],
     "seg_attn_split.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=2"],
 }
 
