@@ -513,6 +513,7 @@ __host__ __device__ __forceinline__ Unit split_unit(const RoundSplit& t, int32_t
     u.parts = 2;
     u.record = 2 * c;
     u.counter = c;
+    u.arrive = 1;
     return u;
   }
   u.item = k - t.two;  // whole items after the parts: k - 2 two + two
@@ -780,11 +781,11 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Spins of the merging part's wait for the other part's record (each
-// s_sleep 1, ~64 cycles): the other part has counted itself in and is
-// resident, so its record lands within microseconds; the bound only keeps
-// the wait finite.
-constexpr int32_t kReadySpins = 1 << 22;
+// Spins of the merging part's wait for the other part's record (each an
+// agent-scope load and s_sleep 8, ~512 cycles): the other part has counted
+// itself in and is resident, so its record lands within microseconds; the
+// bound only keeps the wait finite.
+constexpr int32_t kReadySpins = 1 << 20;
 
 // Part of a cut item: publish the partial record, count it in, and if it is
 // the item's last part to finish, merge every part and write the output.
@@ -793,16 +794,16 @@ constexpr int32_t kReadySpins = 1 << 22;
 // output goes through `stage` (32 * kOutPitch bytes per wave) when
 // kStageOut, else straight from registers.
 //
-// With un.arrive (plans of more units than resident slots, whose two parts
-// mostly run at different times) the two parts count themselves in first:
-// the first to arrive writes its record and then adds a second time
-// (ready); the second writes no record of its own -- it waits until the
-// counter shows both arrivals and the ready mark (3), then merges from its
-// registers and the other record (2B final step 298.9 vs 300.7 us, sweep
-// scale 11 117.0 vs 120.2 us).  Otherwise (parts that run side by side in
-// one round: there the waiting part would only wait for the other's record;
-// sweep scale 9 38.6 vs 34.6 us) every part publishes its record before
-// counting in, and the last to count merges.
+// With un.arrive (every cut unit of the library's plans and round split)
+// the two parts count themselves in first: the first to arrive writes its
+// record and then adds a second time (ready); the second writes no record
+// of its own -- it waits until the counter shows both arrivals and the
+// ready mark (3), then merges from its registers and the other record
+// (2B final step 298.9 vs 300.7 us, sweep scale 11 117.0 vs 120.2 us; with
+// each counter on a line of its own also where the parts run side by side:
+// sweep scale 9 33.1 vs 34.5 us, scale 8 20.1 vs 20.5 us).  Without it
+// every part publishes its record before counting in, and the last to count
+// merges.
 template <int QDT, int kThreads, bool kStageOut = true>
 __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc, const Unit& un,
                                             int32_t parts, const f32x16_t (&oacc)[4], float m_run,
@@ -812,6 +813,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   int32_t* const counters = static_cast<int32_t*>(a.workspace);
   float* const records = reinterpret_cast<float*>(static_cast<uint8_t*>(a.workspace) + kCounterBytes);
   float* const rec0 = records + static_cast<int64_t>(un.record) * (66 * kThreads);
+  int32_t* const counter = counters + static_cast<int64_t>(un.counter) * kCounterStride;
   auto publish = [&]() {
     float* const mine = rec0 + static_cast<int64_t>(un.part) * (66 * kThreads);
 #pragma unroll
@@ -825,27 +827,26 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   };
   if (parts == 2 && un.arrive != 0) {
     if (tid == 0)
-      merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      merge_turn = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (merge_turn == 0) {
       // first to arrive: publish, then the ready mark
       publish();
       if (tid == 0)
-        __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     if (tid == 0) {
       for (int32_t i = 0; i < kReadySpins; ++i) {
-        if (__hip_atomic_load(counters + un.counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3) break;
-        __builtin_amdgcn_s_sleep(1);
+        if (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3) break;
+        __builtin_amdgcn_s_sleep(8);
       }
     }
     __syncthreads();
   } else {
     publish();
     if (tid == 0)
-      merge_turn = __hip_atomic_fetch_add(counters + un.counter, 1, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+      merge_turn = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
     __syncthreads();
     if (!merge_turn) return;
   }
@@ -897,7 +898,7 @@ __device__ __forceinline__ void merge_parts(const AttnArgs& a, const Scalars& sc
   } else {
     write_output(acc, m_new, l_acc, sc.c, a.out, a.lse, w.b, w.h, qrow, L, H, w.bh, g, a.out_dtype);
   }
-  if (tid == 0) __hip_atomic_store(counters + un.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The current rows' append (AttnArgs::append_offsets, and the second

@@ -101,9 +101,8 @@ struct AttnArgs {
 // Work plan units (build_attention_plan): head, index in the head
 // (b * n_qt + qt), key tiles [t0, t1), cut item (-1 = whole), part, 1
 // when the launch's items differ in length (the 16-bit kernel then
-// alternates its wave priority by tile) else 0, and 1 when the plan has more
-// units than resident slots (a cut item's parts count in before publishing:
-// attn::merge_parts) else 0.
+// alternates its wave priority by tile) else 0, and 1 in cut units (the
+// item's parts count in before publishing: attn::merge_parts) else 0.
 constexpr int kPlanInts = 8;
 int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends, const int32_t* seg_counts,
                              int32_t H, int32_t S, int64_t cap, int32_t B, int32_t L, int32_t bm, int32_t slots,
@@ -121,10 +120,14 @@ constexpr int kMaxSegments = 256;
 
 // Round split of the 16-bit attention kernel (workspace layout): kCounterBytes
 // of int32 counters (one per cut item, at most one per resident workgroup
-// slot, 2 slots per CU), then two partial records per slot of kPartialFloats
-// floats (unnormalized O, running max and sum of 128 queries x 256 threads).
+// slot, 2 slots per CU; each on a 64-byte line of its own, kCounterStride
+// ints apart: the atomics of different items on one line serialize), then two
+// partial records per slot of kPartialFloats floats (unnormalized O, running
+// max and sum of 128 queries x 256 threads).
 constexpr int kPartialFloats = 66 * 256;
-constexpr int64_t kCounterBytes = 64 * 1024;  // up to 16384 slots
+constexpr int64_t kCounterBytes = 64 * 1024;
+constexpr int32_t kCounterStride = 16;
+constexpr int32_t kMaxCounters = static_cast<int32_t>(kCounterBytes / 4 / kCounterStride);  // 1024
 int32_t split_slots(int device);  // 0 when the device cannot be queried
 int64_t split_workspace_bytes(int32_t slots);
 

@@ -305,9 +305,8 @@ int32_t build_attention_plan(const int32_t* seg_starts, const int32_t* seg_ends,
       o[5] = x->part;
     }
     o[6] = x == nullptr ? 0 : shared;
-    // more units than slots: a cut item's two parts mostly run at different
-    // times, so they count in first and the second writes no record
-    o[7] = x != nullptr && slots > 0 && n_units > slots ? 1 : 0;
+    // a cut item's two parts count in first; the second writes no record
+    o[7] = x != nullptr && x->cut >= 0 ? 1 : 0;
   };
   if (lists.size() == 1) {
     const std::vector<Unit>& l = lists[0];

@@ -475,7 +475,7 @@ int32_t slots_of(int device) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
       return 0;
-    cache[device] = 2 * cus < 16384 ? 2 * cus : 16384;  // counters fit kCounterBytes
+    cache[device] = 2 * cus < kMaxCounters ? 2 * cus : kMaxCounters;  // a counter per slot
   }
   return cache[device];
 }
@@ -497,7 +497,7 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   b.ws_cuts = 0;
   if (a.workspace != nullptr && a.workspace_bytes > kCounterBytes) {
     const int64_t by_records = (a.workspace_bytes - kCounterBytes) / (2LL * kPartialFloats * 4);
-    b.ws_cuts = static_cast<int32_t>(by_records < kCounterBytes / 4 ? by_records : kCounterBytes / 4);
+    b.ws_cuts = static_cast<int32_t>(by_records < kMaxCounters ? by_records : kMaxCounters);
   }
   // the fused append's copy blocks follow the attention workgroups
   const int64_t copies = a.append_offsets != nullptr ? append_blocks(a.batch, a.heads, a.cur_len) : 0;

@@ -452,7 +452,7 @@ hipError_t launch(const AttnArgs& a, const Scalars& s, hipStream_t st) {
   b.ws_cuts = 0;
   if (a.workspace != nullptr && a.workspace_bytes > kCounterBytes) {
     const int64_t by_records = (a.workspace_bytes - kCounterBytes) / (2LL * 66 * kSThreads * 4);
-    b.ws_cuts = static_cast<int32_t>(by_records < kCounterBytes / 4 ? by_records : kCounterBytes / 4);
+    b.ws_cuts = static_cast<int32_t>(by_records < kMaxCounters ? by_records : kMaxCounters);
   }
   const int64_t grid = a.plan != nullptr ? a.plan_units : items;
   if (grid <= 0) return hipSuccess;

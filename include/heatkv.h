@@ -275,9 +275,10 @@ int32_t hkv_segmented_attention_call(const void* bound, const void* q, void* sla
  * (1 when the items' key tile counts differ by more than 5/4: the 16-bit
  * kernel then alternates its wave priority by tile so the two workgroups of a
  * CU share its SIMDs evenly; 0 otherwise and in empty units), and a flag (1
- * when the plan has more units than slots: a cut item's two parts then count
- * in before the first publishes its partial result and the second merges
- * without publishing its own; 0 otherwise and in empty units).
+ * in every cut unit: the item's two parts count in before the first to
+ * arrive publishes its partial result, and the second merges without
+ * publishing its own; 0 in whole and empty units; a plan may also carry 0 in
+ * cut units, whose parts then both publish and the last to count in merges).
  * Host-only: no device call.  No counterpart in the reference (its tables
  * are the whole plan: the Triton grid walks them).
  */

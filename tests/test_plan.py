@@ -45,14 +45,13 @@ def _check(plan, st, en, ct, B, L, cap, slots):
     # field 6: 1 in every unit when the items' tile counts differ by more
     # than 5/4 (the kernel then shares each CU tile by tile), else 0
     shared = int(4 * max(tiles.values()) > 5 * min(tiles.values())) if tiles else 0
-    # field 7: 1 in every unit of a plan with more units than slots (a cut
-    # item's parts count in before publishing), else 0
-    arrive = int(slots > 0 and len(plan) > slots)
+    # field 7: 1 in every cut unit (its item's parts count in before
+    # publishing: arrival-first merge), 0 in whole ones
     for h, j, t0, t1, cut, part, z0, z1 in plan.tolist():
         if h == -1:  # an empty unit
             assert (j, t0, t1, cut, part, z0, z1) == (-1, 0, 0, -1, 0, 0, 0)
             continue
-        assert 0 <= h < H and 0 <= j < B * n_qt and z0 == shared and z1 == arrive
+        assert 0 <= h < H and 0 <= j < B * n_qt and z0 == shared and z1 == int(cut >= 0)
         assert 0 <= t0 < t1 <= tiles[h]
         cover.setdefault((h, j), []).append((t0, t1))
         if cut >= 0:
