@@ -32,7 +32,6 @@ Differences from the reference, all deliberate:
 from __future__ import annotations
 
 import ctypes
-import os
 from typing import Optional, Tuple
 
 import torch
@@ -42,7 +41,7 @@ from . import _lib
 
 def _positive_int_env(name: str, default: int) -> int:
     """Integer env knob, falling back to ``default`` (real_pruning_fused_attention.py:274-283)."""
-    raw = os.environ.get(name)
+    raw = _lib.env_get(name)
     if raw is None:
         return int(default)
     try:
@@ -54,7 +53,7 @@ def _positive_int_env(name: str, default: int) -> int:
 
 def _fused_value_dot_mode_id() -> int:
     """PV dot mode knob (real_pruning_fused_attention.py:286-295)."""
-    mode = os.environ.get("REAL_PRUNING_FUSED_VALUE_DOT_MODE", "bf16").strip().lower()
+    mode = _lib.env_get("REAL_PRUNING_FUSED_VALUE_DOT_MODE", "bf16").strip().lower()
     if mode in {"bf16", "flash"}:
         return 0
     if mode in {"fp32", "ieee", "mixed", "fp32_probs"}:
@@ -64,7 +63,7 @@ def _fused_value_dot_mode_id() -> int:
 
 def _fused_qk_dot_mode_id() -> int:
     """QK dot mode knob (real_pruning_fused_attention.py:298-308)."""
-    mode = os.environ.get("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16").strip().lower()
+    mode = _lib.env_get("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16").strip().lower()
     if mode in {"bf16", "tensorcore"}:
         return 0
     if mode in {"tf32", "fp32_tf32"}:
@@ -136,7 +135,7 @@ def _split_rows_path(q_dtype, k_dtype, v_dtype, qk_mode: int, value_mode: int) -
     """fp32 q/k with 16-bit v at dot modes other than fp32 run the split-row
     kernel: K is first written as split rows (hkv_split_rows).  HKV_ATTN_SPLIT_ROWS=0
     keeps them on the register-staged kernel (for comparisons)."""
-    if os.environ.get("HKV_ATTN_SPLIT_ROWS", "1").strip().lower() in {"0", "false", "no", "off"}:
+    if _lib.env_get("HKV_ATTN_SPLIT_ROWS", "1").strip().lower() in {"0", "false", "no", "off"}:
         return False
     return (q_dtype == torch.float32 and k_dtype == torch.float32 and v_dtype in (torch.float16, torch.bfloat16)
             and qk_mode != 2 and value_mode != 2)

@@ -33,6 +33,7 @@ from typing import Callable, Dict, Mapping, Optional, Set, Tuple
 
 import torch
 
+from . import _lib
 from . import phase_profile as prof
 from .real_pruning_fused_attention import (
     BoundPack,
@@ -50,7 +51,7 @@ RemovedLookup = Callable[[int], Mapping[int, Set[int]]]
 
 
 def _env_flag(name: str, default: bool) -> bool:
-    raw = os.environ.get(name)
+    raw = _lib.env_get(name)
     if raw is None:
         return default
     return raw.strip().lower() not in {"0", "false", "no", "off"}
@@ -86,7 +87,7 @@ def _capturing() -> bool:
 
 def fused_softmax_mode() -> str:
     """REAL_PRUNING_FUSED_SOFTMAX_MODE, 'exp' or 'exp2' (enable_real_pruning_fast.py:166-170)."""
-    mode = os.environ.get("REAL_PRUNING_FUSED_SOFTMAX_MODE", "exp")
+    mode = _lib.env_get("REAL_PRUNING_FUSED_SOFTMAX_MODE", "exp")
     return mode if mode in {"exp", "exp2"} else "exp"
 
 

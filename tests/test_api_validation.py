@@ -165,3 +165,21 @@ def test_item_shape_helpers_follow_promotion(monkeypatch):
     monkeypatch.setenv("REAL_PRUNING_FUSED_QK_DOT_MODE", "bf16")
     # the default mode refuses mixed q/k; the helpers answer for the dtypes as given
     assert attention_queries_per_item(bf16, f32, bf16) == 128
+
+
+def test_env_get_matches_os_environ(monkeypatch):
+    """The knob reader sees what os.environ.get sees: unset, set, changed,
+    empty and deleted values, and the default."""
+    import os
+
+    from heatkv_amd._lib import env_get
+
+    name = "HKV_TEST_ENV_GET_KNOB"
+    monkeypatch.delenv(name, raising=False)
+    assert env_get(name) is None and env_get(name, "d") == "d"
+    for value in ("1", "0", "", "fp32", "é"):
+        monkeypatch.setenv(name, value)
+        assert env_get(name) == os.environ.get(name) == value
+        assert env_get(name, "d") == value
+    monkeypatch.delenv(name)
+    assert env_get(name, "d") == "d" == os.environ.get(name, "d")
